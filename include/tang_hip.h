@@ -1,0 +1,227 @@
+/*
+ * tang_hip.h -- C ABI of the MI355X (gfx950) backend for tang-compute's
+ * quantized-inference decode path.
+ *
+ * The entry points mirror `tang_compute::ComputeDevice`
+ * (crates/tang-compute/src/device.rs:19-869) for the ops a decode step uses,
+ * plus quantized-linear, MoE and MLA extensions the reference trait lacks.
+ * A Rust `HipComputeDevice: ComputeDevice` forwards to these functions.
+ *
+ * Conventions
+ *  - Every function returns an int status: TH_OK (0) or a TH_ERR_* code; the
+ *    message of the last failure on the calling thread is th_last_error().
+ *    Nothing unwinds across the ABI (the reference panics instead).
+ *  - One device handle per host thread; each device owns one HIP stream.
+ *    Calls enqueue work and return; th_sync / th_buffer_download synchronise
+ *    (device.rs:367 sync, device.rs:75 download).
+ *  - Outputs are caller-allocated buffers (the reference returns owned
+ *    buffers; the shim allocates them with th_buffer_alloc first).
+ *  - Sizes are element counts (usize in the reference).
+ */
+#ifndef TANG_HIP_H
+#define TANG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TH_OK 0
+#define TH_ERR_INVALID 1     /* bad argument, shape or dtype */
+#define TH_ERR_HIP 2         /* HIP runtime error */
+#define TH_ERR_OOM 3         /* device allocation failed */
+#define TH_ERR_UNSUPPORTED 4 /* valid request this backend does not implement */
+
+typedef enum {
+    TH_F32 = 0,
+    TH_BF16 = 1,
+    TH_F16 = 2,
+    TH_U8 = 3,
+    TH_I8 = 4,
+    TH_U32 = 5,
+    TH_I32 = 6
+} th_dtype;
+
+typedef struct th_device th_device;
+typedef struct th_buffer th_buffer;
+typedef struct th_qweight th_qweight;
+
+/* Reference block layouts (crates/tang-infer/src/quantize.rs:15-29), as plain
+ * C structs: Q8Block {scale; values[32]} and Q4Block {scale; values[16]} with
+ * values[i] = (q[2i]+8) | (q[2i+1]+8) << 4. */
+typedef struct { float scale; int8_t values[32]; } th_q8_block;
+typedef struct { float scale; uint8_t values[16]; } th_q4_block;
+
+/* ---- errors, devices, streams ------------------------------------------ */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* th_last_error(void);
+/* Number of visible HIP devices. */
+int th_device_count(int* n);
+/* CudaComputeDevice::new (crates/tang-compute/src/cuda.rs:151). */
+int th_device_create(int ordinal, th_device** out);
+int th_device_destroy(th_device* dev);
+/* ComputeDevice::sync (device.rs:367): wait for all work on the device stream. */
+int th_sync(th_device* dev);
+/* ComputeDevice::total_memory_bytes / free_memory_bytes (device.rs:27-30). */
+int th_memory_info(th_device* dev, size_t* free_bytes, size_t* total_bytes);
+/* Time the work enqueued between start and stop on the device stream with HIP
+ * events; stop synchronises and returns elapsed milliseconds. */
+int th_timer_start(th_device* dev);
+int th_timer_stop(th_device* dev, float* ms);
+
+/* ---- buffers (device.rs:44-80 upload/upload_u32/alloc/download) -------- */
+
+int th_buffer_alloc(th_device* dev, th_dtype dtype, size_t n, th_buffer** out);
+int th_buffer_free(th_buffer* buf);
+/* Copy n elements of the buffer's dtype from host memory (synchronous). */
+int th_buffer_upload(th_buffer* buf, const void* host, size_t n);
+/* Copy n elements to host memory; synchronises the device stream first. */
+int th_buffer_download(th_buffer* buf, void* host, size_t n);
+int th_buffer_info(const th_buffer* buf, th_dtype* dtype, size_t* n);
+/* ComputeDevice::zero_buffer. */
+int th_buffer_zero(th_buffer* buf);
+/* Element-wise dtype conversion between f32, bf16 and f16 buffers of equal
+ * length; f32->bf16 rounds as crates/tang-compute/src/cuda.rs:22-27,
+ * f32->f16 is IEEE round-to-nearest-even (kernels BF16_TO_F32_CUDA /
+ * F32_TO_BF16_CUDA, util_cuda.rs:85,99). */
+int th_convert(th_device* dev, const th_buffer* src, th_buffer* dst);
+
+/* ---- quantized weights ------------------------------------------------- */
+
+/* Upload a row-by-row quantized Q4 matrix in the reference block layout
+ * (quantize_matrix_q4, quantize.rs:208): rows*ceil(cols/32) blocks.
+ * scale_dtype TH_F32 keeps the f32 scales; TH_F16 stores them as f16 and
+ * fails unless every scale is exactly representable. */
+int th_q4_upload_blocks(th_device* dev, const th_q4_block* blocks, size_t rows, size_t cols,
+                        th_dtype scale_dtype, th_qweight** out);
+/* Same matrix as arrays: nib[rows][ceil(cols/32)*16] packed exactly like
+ * Q4Block.values, scales[rows][ceil(cols/32)] of scale_dtype (f32 or f16). */
+int th_q4_upload_packed(th_device* dev, const uint8_t* nib, const void* scales, th_dtype scale_dtype,
+                        size_t rows, size_t cols, th_qweight** out);
+/* Q8 (quantize_matrix_q8, quantize.rs:193), rows*ceil(cols/32) blocks. */
+int th_q8_upload_blocks(th_device* dev, const th_q8_block* blocks, size_t rows, size_t cols,
+                        th_qweight** out);
+/* Q8 with one f32 scale per row: q[rows][cols], row_scale[rows].  Equivalent
+ * to Q8 blocks whose scales within a row are all equal. */
+int th_q8_upload_rowwise(th_device* dev, const int8_t* q, const float* row_scale, size_t rows,
+                         size_t cols, th_qweight** out);
+/* Read a Q4 weight back in the reference block layout (bit-exact round trip). */
+int th_q4_download_blocks(const th_qweight* w, th_q4_block* blocks);
+int th_qweight_info(const th_qweight* w, size_t* rows, size_t* cols, int* bits);
+int th_qweight_free(th_qweight* w);
+
+/* ---- quantized linear ---------------------------------------------------
+ * y[m][n] = sum_k x[m][k] * dequant(W)[n][k]: the quantized form of
+ * ComputeDevice::matmul_b_transposed (device.rs:407) with B = W [n,k]
+ * row-major, i.e. Linear::forward_2d (modules.rs:56) without bias, and
+ * m independent q4_matvec / q8_matvec calls (quantize.rs:227-289).
+ * x: f32 or bf16 [m][k]; y: f32 [m][n].  Accumulation is f32. */
+int th_gemm_q4(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y);
+int th_gemv_q8(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y);
+
+/* ---- decode ops (f32 buffers unless stated) ---------------------------- */
+
+/* CpuDevice::rms_norm (crates/tang-compute/src/cpu.rs:126); weight f32 or bf16. */
+int th_rms_norm(th_device* dev, const th_buffer* x, const th_buffer* weight, size_t n_groups,
+                size_t dim, float eps, th_buffer* out);
+/* ComputeDevice::rms_norm_residual (device.rs:546): out = norm(in+res),
+ * sum_out = in+res. */
+int th_rms_norm_residual(th_device* dev, const th_buffer* in, const th_buffer* residual,
+                         const th_buffer* weight, size_t n_groups, size_t dim, float eps,
+                         th_buffer* out, th_buffer* sum_out);
+/* InterleavedRoPE::new tables (modules.rs:495-511), host-side:
+ * cos/sin [max_seq][head_dim/2]. */
+int th_rope_tables(size_t head_dim, size_t max_seq, double base, float* cos_table, float* sin_table);
+/* ComputeDevice::rope_forward_cached (device.rs:678 -> :582). */
+int th_rope_forward(th_device* dev, const th_buffer* in, const th_buffer* cos_buf,
+                    const th_buffer* sin_buf, size_t seq_len, size_t n_heads, size_t head_dim,
+                    size_t start_pos, th_buffer* out);
+/* ComputeDevice::kv_attention (cpu.rs:257): q [q_len][n_heads*head_dim] f32,
+ * caches [>= cache_start+q_len][n_kv_heads*head_dim] of f32 or f16; query i
+ * attends to positions 0..cache_start+i.  No length limit. */
+int th_kv_attention(th_device* dev, const th_buffer* q, const th_buffer* k_cache,
+                    const th_buffer* v_cache, size_t cache_start, size_t q_len, size_t n_heads,
+                    size_t n_kv_heads, size_t head_dim, th_buffer* out);
+/* swiglu_fused_buf (device.rs:727): out = g*sigmoid(g)*u. */
+int th_swiglu(th_device* dev, const th_buffer* gate, const th_buffer* up, size_t n, th_buffer* out);
+/* add_tensors_buf (device.rs:721). */
+int th_add(th_device* dev, const th_buffer* a, const th_buffer* b, size_t n, th_buffer* out);
+/* CpuDevice::embedding (cpu.rs:151): weight f32 or bf16 [vocab][dim], ids u32. */
+int th_embedding(th_device* dev, const th_buffer* weight, const th_buffer* ids, size_t seq_len,
+                 size_t dim, th_buffer* out);
+/* CpuDevice::softmax (cpu.rs:105). */
+int th_softmax(th_device* dev, const th_buffer* x, size_t n_rows, size_t row_len, th_buffer* out);
+/* Greedy Sampler argmax (crates/tang-infer/src/sampling.rs:184): first
+ * maximum wins.  x f32 [n_rows][n]; out u32 [n_rows]. */
+int th_argmax(th_device* dev, const th_buffer* x, size_t n_rows, size_t n, th_buffer* out);
+
+/* ---- device-resident Llama-style decode engine --------------------------
+ * The decode step of crates/tang-train/examples/smollm.rs:215-300 with every
+ * linear int4 group-32, bf16 embeddings and norm weights, and an f16 KV cache
+ * kept on the device.  Greedy loop as crates/tang-infer/src/sampling.rs:229. */
+typedef struct {
+    int n_layers, d_model, n_heads, n_kv_heads, head_dim, d_ff, vocab, max_seq;
+    float eps;
+    double rope_theta;
+} th_llama_config;
+typedef struct th_llama th_llama;
+
+int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out);
+int th_llama_destroy(th_llama* m);
+/* Fill all weights with the seeded synthetic generator (th_synth_*): linear
+ * tensor t of layer l uses seed th_synth_seed(seed, l, t). */
+int th_llama_init_synthetic(th_llama* m, uint64_t seed);
+/* Fill KV positions [0, len) of every layer with N(0,1) f16 values. */
+int th_llama_fill_kv_synthetic(th_llama* m, size_t len, uint64_t seed);
+/* Greedy decode: feed `token` at position `pos`, then n_steps-1 more steps on
+ * the argmax; tokens_out[i] is the argmax after step i.  last_logits (may be
+ * NULL) receives the final step's f32 logits [vocab]. */
+int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, int32_t* tokens_out,
+                      float* last_logits);
+/* One decode step without host round-trips, for timing: token is read from
+ * and argmax written to the model's device-side token slot. */
+int th_llama_step_device(th_llama* m, size_t pos);
+int th_llama_set_token(th_llama* m, int32_t token);
+
+/* ---- MoE (DeepSeek-style; no reference implementation) ------------------ */
+typedef struct th_moe th_moe;
+int th_moe_create(th_device* dev, size_t d_model, size_t d_ff, size_t n_experts, size_t n_shared,
+                  size_t top_k, th_moe** out);
+int th_moe_destroy(th_moe* moe);
+/* Router W ~ N(0,0.02) f32 [E][d]; expert linears int4 g32 from th_synth_q4. */
+int th_moe_init_synthetic(th_moe* moe, uint64_t seed);
+/* h bf16 [T][d] -> out f32 [T][d]; topk_idx i32 [T][k], topk_w f32 [T][k]. */
+int th_moe_forward(th_moe* moe, const th_buffer* h, size_t T, th_buffer* out, th_buffer* topk_idx,
+                   th_buffer* topk_w);
+
+/* ---- MLA decode attention (absorbed; no reference implementation) ------ */
+/* q_nope f32 [B][H][dn], q_rope f32 [B][H][dr], cache bf16 [B][L][r+dr];
+ * w_uk Q8 rowwise [H*r][dn]; w_uv Q8 rowwise [H*dv][r]; out f32 [B][H][dv]. */
+int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_buffer* q_rope,
+                  const th_buffer* cache, size_t B, size_t H, size_t L, size_t dn, size_t dr,
+                  size_t r, size_t dv, const th_qweight* w_uk, const th_qweight* w_uv,
+                  float sm_scale, th_buffer* out);
+
+/* ---- seeded synthetic data (host) ---------------------------------------
+ * xoshiro256** seeded through SplitMix64, as crates/tang-bench/src/lib.rs:7-46.
+ * uniform(a,b) = a + (b-a)*(f64()+1)/2 with f64() the reference's [-1,1] map;
+ * normal = Box-Muller on two 53-bit uniforms. */
+uint64_t th_synth_seed(uint64_t base, uint64_t layer, uint64_t tensor);
+/* Packed int4: every byte is one draw-byte (two nibbles ~U[0,15], value-8 in
+ * [-8,7]); scales f16 ~U[smin,smax] rounded to nearest. */
+int th_synth_q4(uint64_t seed, size_t rows, size_t cols, float smin, float smax, uint8_t* nib,
+                uint16_t* scales_f16);
+/* int8 ~U[-127,127] and per-row f32 scales ~U[smin,smax]. */
+int th_synth_q8_rowwise(uint64_t seed, size_t rows, size_t cols, float smin, float smax, int8_t* q,
+                        float* row_scale);
+/* N(0,std) values rounded to bf16 / f16 / f32 (dtype TH_BF16/TH_F16/TH_F32). */
+int th_synth_normal(uint64_t seed, size_t n, float std, th_dtype dtype, void* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TANG_HIP_H */

@@ -1,0 +1,261 @@
+"""CPU oracle: ctypes binding of oracle/liboracle.so (oracle/tang_oracle.c).
+
+TEST INFRASTRUCTURE ONLY -- the restatement of the reference's CPU
+arithmetic that the HIP path is checked against.  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+Q4_BLOCK = np.dtype([("scale", "<f4"), ("values", "u1", (16,))])
+Q8_BLOCK = np.dtype([("scale", "<f4"), ("values", "i1", (32,))])
+
+_P, _S, _I, _F, _D = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_double
+
+
+class LlamaCfg(ctypes.Structure):
+    _fields_ = [("n_layers", _I), ("d_model", _I), ("n_heads", _I), ("n_kv_heads", _I), ("head_dim", _I),
+                ("d_ff", _I), ("vocab", _I), ("max_seq", _I), ("eps", _F)]
+
+
+class Q4View(ctypes.Structure):
+    _fields_ = [("nib", _P), ("scales", _P)]
+
+
+class LlamaWeights(ctypes.Structure):
+    _fields_ = [("embed", _P), ("attn_norm", _P), ("ffn_norm", _P), ("final_norm", _P),
+                ("wq", _P), ("wk", _P), ("wv", _P), ("wo", _P), ("wg", _P), ("wu", _P), ("wd", _P),
+                ("lm_head", Q4View), ("rope_cos", _P), ("rope_sin", _P)]
+
+
+_SIG = {
+    "or_f32_to_bf16": ([_F], ctypes.c_uint16),
+    "or_bf16_to_f32": ([ctypes.c_uint16], _F),
+    "or_f16_to_f32": ([ctypes.c_uint16], _F),
+    "or_f32_to_f16": ([_F], ctypes.c_uint16),
+    "or_f32_to_bf16_array": ([_P, _S, _P], None),
+    "or_bf16_to_f32_array": ([_P, _S, _P], None),
+    "or_f16_to_f32_array": ([_P, _S, _P], None),
+    "or_f32_to_f16_array": ([_P, _S, _P], None),
+    "or_quantize_q8": ([_P, _S, _P], _S),
+    "or_dequantize_q8": ([_P, _S, _P], None),
+    "or_quantize_q4": ([_P, _S, _P], _S),
+    "or_dequantize_q4": ([_P, _S, _P], None),
+    "or_quantize_matrix_q8": ([_P, _S, _S, _P], _S),
+    "or_quantize_matrix_q4": ([_P, _S, _S, _P], _S),
+    "or_q8_matvec": ([_P, _S, _S, _P, _P], None),
+    "or_q4_matvec": ([_P, _S, _S, _P, _P], None),
+    "or_q4_matvec_soa": ([_P, _P, _S, _S, _P, _P, _I], None),
+    "or_q8_matvec_soa": ([_P, _P, _S, _S, _P, _P, _I], None),
+    "or_rms_norm": ([_P, _P, _S, _S, _F, _P], None),
+    "or_rms_norm_residual": ([_P, _P, _P, _S, _S, _F, _P, _P], None),
+    "or_rope_tables": ([_S, _S, _D, _P, _P], None),
+    "or_rope_forward": ([_P, _P, _P, _S, _S, _S, _S, _P], None),
+    "or_kv_attention": ([_P, _P, _P, _S, _S, _S, _S, _S, _P, _I], None),
+    "or_swiglu": ([_P, _P, _S, _P], None),
+    "or_add": ([_P, _P, _S, _P], None),
+    "or_embedding": ([_P, _P, _S, _S, _P], None),
+    "or_softmax": ([_P, _S, _S, _P], None),
+    "or_argmax_f32": ([_P, _S], _S),
+    "or_llama_decode_step": ([_P, _P, _P, _P, _I, _I, _P, _I], _I),
+    "or_moe_forward": ([_P, _S, _S, _S, _S, _S, _S, _P, _P, _P, _P, _P, _P, _I], None),
+    "or_mla_decode": ([_P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _P, _P, _D, _P, _I], None),
+}
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        for n, (a, r) in _SIG.items():
+            f = getattr(L, n)
+            f.argtypes = a
+            f.restype = r
+        _lib = L
+    return _lib
+
+
+def p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def f32_to_bf16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_bf16_array(p(x), x.size, p(out))
+    return out
+
+
+def bf16_to_f32(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().or_bf16_to_f32_array(p(h), h.size, p(out))
+    return out
+
+
+def f16_to_f32(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().or_f16_to_f32_array(p(h), h.size, p(out))
+    return out
+
+
+def f32_to_f16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_f16_array(p(x), x.size, p(out))
+    return out
+
+
+def quantize_q4(data):
+    data = np.ascontiguousarray(data, np.float32)
+    out = np.zeros((data.size + 31) // 32, Q4_BLOCK)
+    lib().or_quantize_q4(p(data), data.size, p(out))
+    return out
+
+
+def dequantize_q4(blocks):
+    out = np.empty(blocks.size * 32, np.float32)
+    lib().or_dequantize_q4(p(blocks), blocks.size, p(out))
+    return out
+
+
+def quantize_q8(data):
+    data = np.ascontiguousarray(data, np.float32)
+    out = np.zeros((data.size + 31) // 32, Q8_BLOCK)
+    lib().or_quantize_q8(p(data), data.size, p(out))
+    return out
+
+
+def dequantize_q8(blocks):
+    out = np.empty(blocks.size * 32, np.float32)
+    lib().or_dequantize_q8(p(blocks), blocks.size, p(out))
+    return out
+
+
+def quantize_matrix_q4(data, rows, cols):
+    data = np.ascontiguousarray(data, np.float32)
+    out = np.zeros(rows * ((cols + 31) // 32), Q4_BLOCK)
+    lib().or_quantize_matrix_q4(p(data), rows, cols, p(out))
+    return out
+
+
+def quantize_matrix_q8(data, rows, cols):
+    data = np.ascontiguousarray(data, np.float32)
+    out = np.zeros(rows * ((cols + 31) // 32), Q8_BLOCK)
+    lib().or_quantize_matrix_q8(p(data), rows, cols, p(out))
+    return out
+
+
+def q4_matvec(blocks, rows, cols, x):
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty(rows, np.float64)
+    lib().or_q4_matvec(p(np.ascontiguousarray(blocks)), rows, cols, p(x), p(y))
+    return y
+
+
+def q8_matvec(blocks, rows, cols, x):
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty(rows, np.float64)
+    lib().or_q8_matvec(p(np.ascontiguousarray(blocks)), rows, cols, p(x), p(y))
+    return y
+
+
+def q4_matvec_soa(nib, scales_f32, rows, cols, x, threads=0):
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty(rows, np.float64)
+    lib().or_q4_matvec_soa(p(np.ascontiguousarray(nib)), p(np.ascontiguousarray(scales_f32, np.float32)), rows,
+                           cols, p(x), p(y), threads)
+    return y
+
+
+def q8_matvec_soa(q, scales_f32, rows, cols, x, threads=0):
+    x = np.ascontiguousarray(x, np.float64)
+    y = np.empty(rows, np.float64)
+    lib().or_q8_matvec_soa(p(np.ascontiguousarray(q, np.int8)), p(np.ascontiguousarray(scales_f32, np.float32)),
+                           rows, cols, p(x), p(y), threads)
+    return y
+
+
+def rms_norm(x, w, groups, dim, eps):
+    x = np.ascontiguousarray(x, np.float32); w = np.ascontiguousarray(w, np.float32)
+    out = np.empty(groups * dim, np.float32)
+    lib().or_rms_norm(p(x), p(w), groups, dim, eps, p(out))
+    return out
+
+
+def rms_norm_residual(inp, res, w, groups, dim, eps):
+    a = np.ascontiguousarray(inp, np.float32); b = np.ascontiguousarray(res, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty(groups * dim, np.float32); s = np.empty(groups * dim, np.float32)
+    lib().or_rms_norm_residual(p(a), p(b), p(w), groups, dim, eps, p(out), p(s))
+    return out, s
+
+
+def rope_tables(head_dim, max_seq, base):
+    half = head_dim // 2
+    c = np.empty(max_seq * half, np.float32); s = np.empty(max_seq * half, np.float32)
+    lib().or_rope_tables(head_dim, max_seq, base, p(c), p(s))
+    return c, s
+
+
+def rope_forward(x, cos_t, sin_t, seq_len, n_heads, head_dim, start_pos):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().or_rope_forward(p(x), p(cos_t), p(sin_t), seq_len, n_heads, head_dim, start_pos, p(out))
+    return out
+
+
+def kv_attention(q, k, v, cache_start, q_len, n_heads, n_kv_heads, head_dim, threads=0):
+    q = np.ascontiguousarray(q, np.float32); k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.empty(q_len * n_heads * head_dim, np.float32)
+    lib().or_kv_attention(p(q), p(k), p(v), cache_start, q_len, n_heads, n_kv_heads, head_dim, p(out), threads)
+    return out
+
+
+def swiglu(g, u):
+    g = np.ascontiguousarray(g, np.float32); u = np.ascontiguousarray(u, np.float32)
+    out = np.empty_like(g)
+    lib().or_swiglu(p(g), p(u), g.size, p(out))
+    return out
+
+
+def add(a, b):
+    a = np.ascontiguousarray(a, np.float32); b = np.ascontiguousarray(b, np.float32)
+    out = np.empty_like(a)
+    lib().or_add(p(a), p(b), a.size, p(out))
+    return out
+
+
+def embedding(weight, ids, seq_len, dim):
+    w = np.ascontiguousarray(weight, np.float32); i = np.ascontiguousarray(ids, np.uint32)
+    out = np.empty(seq_len * dim, np.float32)
+    lib().or_embedding(p(w), p(i), seq_len, dim, p(out))
+    return out
+
+
+def softmax(x, rows, length):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().or_softmax(p(x), rows, length, p(out))
+    return out
+
+
+def argmax(x):
+    x = np.ascontiguousarray(x, np.float32)
+    return int(lib().or_argmax_f32(p(x), x.size))

@@ -1,0 +1,368 @@
+"""ctypes binding of the C ABI in include/tang_hip.h.
+
+`HipComputeDevice` mirrors the method names and argument meaning of
+`tang_compute::ComputeDevice` (crates/tang-compute/src/device.rs:19-869) for
+the decode-path ops, plus the quantized extensions.  Errors raise
+`TangHipError` carrying the C status code and th_last_error() text (the
+reference panics instead).
+
+The shared library must have been built (tang_amd/build.py); importing this
+module without it raises, so no caller can silently fall back to CPU code.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtang_hip.so")
+
+TH_OK, TH_ERR_INVALID, TH_ERR_HIP, TH_ERR_OOM, TH_ERR_UNSUPPORTED = 0, 1, 2, 3, 4
+F32, BF16, F16, U8, I8, U32, I32 = range(7)
+
+_NP = {F32: np.float32, BF16: np.uint16, F16: np.uint16, U8: np.uint8, I8: np.int8, U32: np.uint32, I32: np.int32}
+
+Q4_BLOCK = np.dtype([("scale", "<f4"), ("values", "u1", (16,))])
+Q8_BLOCK = np.dtype([("scale", "<f4"), ("values", "i1", (32,))])
+
+
+class TangHipError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("tang_hip error %d: %s" % (code, msg))
+        self.code = code
+
+
+class LlamaConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", ctypes.c_int), ("d_model", ctypes.c_int), ("n_heads", ctypes.c_int),
+        ("n_kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("d_ff", ctypes.c_int),
+        ("vocab", ctypes.c_int), ("max_seq", ctypes.c_int), ("eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_double),
+    ]
+
+
+# Every entry point declared in include/tang_hip.h, with its argument types.
+_P, _S, _U64, _I, _F, _D = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int, ctypes.c_float, ctypes.c_double
+SIGNATURES = {
+    "th_last_error": ([], ctypes.c_char_p),
+    "th_device_count": ([_P], _I),
+    "th_device_create": ([_I, _P], _I),
+    "th_device_destroy": ([_P], _I),
+    "th_sync": ([_P], _I),
+    "th_memory_info": ([_P, _P, _P], _I),
+    "th_timer_start": ([_P], _I),
+    "th_timer_stop": ([_P, _P], _I),
+    "th_buffer_alloc": ([_P, _I, _S, _P], _I),
+    "th_buffer_free": ([_P], _I),
+    "th_buffer_upload": ([_P, _P, _S], _I),
+    "th_buffer_download": ([_P, _P, _S], _I),
+    "th_buffer_info": ([_P, _P, _P], _I),
+    "th_buffer_zero": ([_P], _I),
+    "th_convert": ([_P, _P, _P], _I),
+    "th_q4_upload_blocks": ([_P, _P, _S, _S, _I, _P], _I),
+    "th_q4_upload_packed": ([_P, _P, _P, _I, _S, _S, _P], _I),
+    "th_q8_upload_blocks": ([_P, _P, _S, _S, _P], _I),
+    "th_q8_upload_rowwise": ([_P, _P, _P, _S, _S, _P], _I),
+    "th_q4_download_blocks": ([_P, _P], _I),
+    "th_qweight_info": ([_P, _P, _P, _P], _I),
+    "th_qweight_free": ([_P], _I),
+    "th_gemm_q4": ([_P, _P, _S, _P, _P], _I),
+    "th_gemv_q8": ([_P, _P, _S, _P, _P], _I),
+    "th_rms_norm": ([_P, _P, _P, _S, _S, _F, _P], _I),
+    "th_rms_norm_residual": ([_P, _P, _P, _P, _S, _S, _F, _P, _P], _I),
+    "th_rope_tables": ([_S, _S, _D, _P, _P], _I),
+    "th_rope_forward": ([_P, _P, _P, _P, _S, _S, _S, _S, _P], _I),
+    "th_kv_attention": ([_P, _P, _P, _P, _S, _S, _S, _S, _S, _P], _I),
+    "th_swiglu": ([_P, _P, _P, _S, _P], _I),
+    "th_add": ([_P, _P, _P, _S, _P], _I),
+    "th_embedding": ([_P, _P, _P, _S, _S, _P], _I),
+    "th_softmax": ([_P, _P, _S, _S, _P], _I),
+    "th_argmax": ([_P, _P, _S, _S, _P], _I),
+    "th_llama_create": ([_P, _P, _P], _I),
+    "th_llama_destroy": ([_P], _I),
+    "th_llama_init_synthetic": ([_P, _U64], _I),
+    "th_llama_fill_kv_synthetic": ([_P, _S, _U64], _I),
+    "th_llama_generate": ([_P, ctypes.c_int32, _S, _S, _P, _P], _I),
+    "th_llama_step_device": ([_P, _S], _I),
+    "th_llama_set_token": ([_P, ctypes.c_int32], _I),
+    "th_moe_create": ([_P, _S, _S, _S, _S, _S, _P], _I),
+    "th_moe_destroy": ([_P], _I),
+    "th_moe_init_synthetic": ([_P, _U64], _I),
+    "th_moe_forward": ([_P, _P, _S, _P, _P, _P], _I),
+    "th_mla_decode": ([_P, _P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _F, _P], _I),
+    "th_synth_seed": ([_U64, _U64, _U64], _U64),
+    "th_synth_q4": ([_U64, _S, _S, _F, _F, _P, _P], _I),
+    "th_synth_q8_rowwise": ([_U64, _S, _S, _F, _F, _P, _P], _I),
+    "th_synth_normal": ([_U64, _S, _F, _I, _P], _I),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libtang_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError("tang_amd: %s is missing; run __graft_entry__.build() first" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != TH_OK:
+        raise TangHipError(rc, lib().th_last_error().decode())
+
+
+def ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def device_count():
+    n = ctypes.c_int(0)
+    check(lib().th_device_count(ctypes.byref(n)))
+    return n.value
+
+
+# --------------------------------------------------------------------------
+# host-side generators (product code: the seeded synthetic data of benches)
+# --------------------------------------------------------------------------
+
+def synth_seed(base, layer, tensor):
+    return lib().th_synth_seed(base, layer, tensor)
+
+
+def synth_q4(seed, rows, cols, smin=0.002, smax=0.01):
+    """Packed nibbles [rows][ceil(cols/32)*16] u8 and f16 scales (as u16) [rows][ceil(cols/32)]."""
+    bpr = (cols + 31) // 32
+    nib = np.empty((rows, bpr * 16), np.uint8)
+    sc = np.empty((rows, bpr), np.uint16)
+    check(lib().th_synth_q4(seed, rows, cols, smin, smax, ptr(nib), ptr(sc)))
+    return nib, sc
+
+
+def synth_q8_rowwise(seed, rows, cols, smin=0.005, smax=0.02):
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    check(lib().th_synth_q8_rowwise(seed, rows, cols, smin, smax, ptr(q), ptr(s)))
+    return q, s
+
+
+def synth_normal(seed, n, std=1.0, dtype=F32):
+    out = np.empty(n, _NP[dtype])
+    check(lib().th_synth_normal(seed, n, std, dtype, ptr(out)))
+    return out
+
+
+def rope_tables(head_dim, max_seq, base):
+    half = head_dim // 2
+    c = np.empty(max_seq * half, np.float32)
+    s = np.empty(max_seq * half, np.float32)
+    check(lib().th_rope_tables(head_dim, max_seq, base, ptr(c), ptr(s)))
+    return c, s
+
+
+# --------------------------------------------------------------------------
+# device objects
+# --------------------------------------------------------------------------
+
+class Buffer:
+    def __init__(self, dev, dtype, n):
+        self.dev, self.dtype, self.n = dev, dtype, int(n)
+        h = ctypes.c_void_p()
+        check(lib().th_buffer_alloc(dev.handle, dtype, self.n, ctypes.byref(h)))
+        self.handle = h
+
+    def __len__(self):
+        return self.n
+
+    def upload(self, arr):
+        a = np.ascontiguousarray(arr, dtype=_NP[self.dtype]).reshape(-1)
+        check(lib().th_buffer_upload(self.handle, ptr(a), a.size))
+
+    def to_numpy(self, n=None):
+        n = self.n if n is None else n
+        out = np.empty(n, _NP[self.dtype])
+        check(lib().th_buffer_download(self.handle, ptr(out), n))
+        return out
+
+    def free(self):
+        if self.handle:
+            check(lib().th_buffer_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.th_buffer_free(self.handle)
+        except Exception:
+            pass
+
+
+class QWeight:
+    def __init__(self, handle, rows, cols, bits):
+        self.handle, self.rows, self.cols, self.bits = handle, rows, cols, bits
+
+    def download_q4_blocks(self):
+        bpr = (self.cols + 31) // 32
+        out = np.zeros(self.rows * bpr, Q4_BLOCK)
+        check(lib().th_q4_download_blocks(self.handle, ptr(out)))
+        return out
+
+    def free(self):
+        if self.handle:
+            check(lib().th_qweight_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.th_qweight_free(self.handle)
+        except Exception:
+            pass
+
+
+class HipComputeDevice:
+    """One device handle (one HIP stream), methods named as ComputeDevice's."""
+
+    def __init__(self, ordinal=0):
+        h = ctypes.c_void_p()
+        check(lib().th_device_create(ordinal, ctypes.byref(h)))
+        self.handle = h
+
+    # -- buffer lifecycle (device.rs:44-80)
+    def upload(self, data, dtype=F32):
+        a = np.ascontiguousarray(data, dtype=_NP[dtype]).reshape(-1)
+        b = Buffer(self, dtype, a.size)
+        b.upload(a)
+        return b
+
+    def upload_u32(self, data):
+        return self.upload(data, U32)
+
+    def alloc(self, n, dtype=F32):
+        return Buffer(self, dtype, n)
+
+    def download(self, buf):
+        return buf.to_numpy()
+
+    def sync(self):
+        check(lib().th_sync(self.handle))
+
+    def zero_buffer(self, buf):
+        check(lib().th_buffer_zero(buf.handle))
+
+    def convert(self, src, dtype):
+        out = self.alloc(src.n, dtype)
+        check(lib().th_convert(self.handle, src.handle, out.handle))
+        return out
+
+    def memory_info(self):
+        f, t = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib().th_memory_info(self.handle, ctypes.byref(f), ctypes.byref(t)))
+        return f.value, t.value
+
+    def timer_start(self):
+        check(lib().th_timer_start(self.handle))
+
+    def timer_stop(self):
+        ms = ctypes.c_float()
+        check(lib().th_timer_stop(self.handle, ctypes.byref(ms)))
+        return ms.value
+
+    # -- quantized weights
+    def q4_upload_blocks(self, blocks, rows, cols, scale_dtype=F32):
+        b = np.ascontiguousarray(blocks, Q4_BLOCK)
+        h = ctypes.c_void_p()
+        check(lib().th_q4_upload_blocks(self.handle, ptr(b), rows, cols, scale_dtype, ctypes.byref(h)))
+        return QWeight(h, rows, cols, 4)
+
+    def q4_upload_packed(self, nib, scales, rows, cols, scale_dtype=F16):
+        n = np.ascontiguousarray(nib, np.uint8)
+        s = np.ascontiguousarray(scales, np.uint16 if scale_dtype == F16 else np.float32)
+        h = ctypes.c_void_p()
+        check(lib().th_q4_upload_packed(self.handle, ptr(n), ptr(s), scale_dtype, rows, cols, ctypes.byref(h)))
+        return QWeight(h, rows, cols, 4)
+
+    def q8_upload_blocks(self, blocks, rows, cols):
+        b = np.ascontiguousarray(blocks, Q8_BLOCK)
+        h = ctypes.c_void_p()
+        check(lib().th_q8_upload_blocks(self.handle, ptr(b), rows, cols, ctypes.byref(h)))
+        return QWeight(h, rows, cols, 8)
+
+    def q8_upload_rowwise(self, q, row_scale, rows, cols):
+        qq = np.ascontiguousarray(q, np.int8)
+        s = np.ascontiguousarray(row_scale, np.float32)
+        h = ctypes.c_void_p()
+        check(lib().th_q8_upload_rowwise(self.handle, ptr(qq), ptr(s), rows, cols, ctypes.byref(h)))
+        return QWeight(h, rows, cols, 8)
+
+    # -- quantized linear (matmul_b_transposed with a quantized B, device.rs:407)
+    def gemm_q4(self, x, m, w, y=None):
+        y = y or self.alloc(m * w.rows)
+        check(lib().th_gemm_q4(self.handle, x.handle, m, w.handle, y.handle))
+        return y
+
+    def gemv_q8(self, x, m, w, y=None):
+        y = y or self.alloc(m * w.rows)
+        check(lib().th_gemv_q8(self.handle, x.handle, m, w.handle, y.handle))
+        return y
+
+    # -- decode ops
+    def rms_norm(self, data, weight, n_groups, dim, eps):
+        out = self.alloc(n_groups * dim)
+        check(lib().th_rms_norm(self.handle, data.handle, weight.handle, n_groups, dim, eps, out.handle))
+        return out
+
+    def rms_norm_residual(self, inp, residual, weight, n_groups, dim, eps):
+        out, s = self.alloc(n_groups * dim), self.alloc(n_groups * dim)
+        check(lib().th_rms_norm_residual(self.handle, inp.handle, residual.handle, weight.handle, n_groups, dim,
+                                         eps, out.handle, s.handle))
+        return out, s
+
+    def rope_forward_cached(self, inp, cos_buf, sin_buf, seq_len, n_heads, head_dim, start_pos):
+        out = self.alloc(seq_len * n_heads * head_dim)
+        check(lib().th_rope_forward(self.handle, inp.handle, cos_buf.handle, sin_buf.handle, seq_len, n_heads,
+                                    head_dim, start_pos, out.handle))
+        return out
+
+    def kv_attention(self, q, k_cache, v_cache, cache_start, q_len, n_heads, n_kv_heads, head_dim):
+        out = self.alloc(q_len * n_heads * head_dim)
+        check(lib().th_kv_attention(self.handle, q.handle, k_cache.handle, v_cache.handle, cache_start, q_len,
+                                    n_heads, n_kv_heads, head_dim, out.handle))
+        return out
+
+    def swiglu_fused_buf(self, gate, up, numel):
+        out = self.alloc(numel)
+        check(lib().th_swiglu(self.handle, gate.handle, up.handle, numel, out.handle))
+        return out
+
+    def add_tensors_buf(self, a, b, numel):
+        out = self.alloc(numel)
+        check(lib().th_add(self.handle, a.handle, b.handle, numel, out.handle))
+        return out
+
+    def embedding(self, weight, ids, seq_len, dim):
+        out = self.alloc(seq_len * dim)
+        check(lib().th_embedding(self.handle, weight.handle, ids.handle, seq_len, dim, out.handle))
+        return out
+
+    def softmax(self, data, n_rows, row_len):
+        out = self.alloc(n_rows * row_len)
+        check(lib().th_softmax(self.handle, data.handle, n_rows, row_len, out.handle))
+        return out
+
+    def argmax(self, data, n_rows, n):
+        out = self.alloc(n_rows, U32)
+        check(lib().th_argmax(self.handle, data.handle, n_rows, n, out.handle))
+        return out
+
+    def close(self):
+        if self.handle:
+            check(lib().th_device_destroy(self.handle))
+            self.handle = None

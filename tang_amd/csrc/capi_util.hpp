@@ -1,0 +1,44 @@
+// Helpers shared by the translation units that implement the C ABI.
+#pragma once
+
+#include "common.hpp"
+
+// Wrap a C entry point body: exceptions become status codes + last error.
+#define TH_API_BEGIN try {
+#define TH_API_END                                              \
+    }                                                           \
+    catch (const ::th::Error& e) {                              \
+        ::th::set_last_error(e.what());                         \
+        return e.code;                                          \
+    }                                                           \
+    catch (const std::exception& e) {                           \
+        ::th::set_last_error(e.what());                         \
+        return TH_ERR_INVALID;                                  \
+    }                                                           \
+    catch (...) {                                               \
+        ::th::set_last_error("unknown error");                  \
+        return TH_ERR_INVALID;                                  \
+    }                                                           \
+    ::th::set_last_error("");                                   \
+    return TH_OK;
+
+namespace th {
+
+// Grow-only stream-ordered workspace owned by the device.
+void* device_scratch(th_device* dev, size_t bytes);
+void require_len(const th_buffer* b, th_dtype dt, size_t n, const char* what);
+void require_len_any(const th_buffer* b, size_t n, const char* what);
+
+th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_dtype sdt, size_t rows,
+                    size_t cols);
+th_qweight* q8_pack(th_device* dev, const int8_t* q, size_t ldq, const float* scales, bool per_row,
+                    size_t rows, size_t cols);
+
+// Quantized linear launchers (qlinear.hip).  x: [m][ldx] f32 or bf16,
+// y: [m][ldy] f32.
+void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
+                      size_t ldy, hipStream_t stream, th_device* dev);
+void launch_q8_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
+                      size_t ldy, hipStream_t stream);
+
+}  // namespace th

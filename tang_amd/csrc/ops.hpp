@@ -1,0 +1,101 @@
+// Device helpers shared by the row-wise op kernels and the decode engine.
+#pragma once
+
+#include <cmath>
+#include <vector>
+
+#include "common.hpp"
+
+namespace th {
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
+    // crates/tang-compute/src/cuda.rs:22-27
+    uint32_t b = __float_as_uint(v);
+    b += 0x7FFFu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+__device__ __forceinline__ float load_w(const void* w, int bf16, size_t i) {
+    return bf16 ? __uint_as_float((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i];
+}
+
+// Wave-level sum: row-local DPP-free butterfly over 64 lanes.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum over a 256-thread block; every thread gets the result.
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = (red[0] + red[1]) + (red[2] + red[3]);
+    return s;
+}
+__device__ __forceinline__ float block_max_256(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// out = g * sigmoid(g) * u evaluated in f64 and stored as f32, as the
+// reference's elementwise closure (device.rs:727-736 via cpu.rs:68-97).
+__device__ __forceinline__ float swiglu_f64(float g, float u) {
+    const double gd = (double)g;
+    const double sig = 1.0 / (1.0 + exp(-gd));
+    return (float)(gd * sig * (double)u);
+}
+
+// First-maximum argmax over one row with a 256-thread block
+// (crates/tang-infer/src/sampling.rs:184-194: strict '>' keeps the lowest index).
+__device__ __forceinline__ void argmax_block_256(const float* x, int n, float* rv, int* ri, float& bv_out, int& bi_out) {
+    float bv = -INFINITY;
+    int bi = n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > bv) { bv = v; bi = i; }
+    }
+    rv[threadIdx.x] = bv;
+    ri[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const float ov = rv[threadIdx.x + s];
+            const int oi = ri[threadIdx.x + s];
+            const float mv = rv[threadIdx.x];
+            const int mi = ri[threadIdx.x];
+            if (ov > mv || (ov == mv && oi < mi)) { rv[threadIdx.x] = ov; ri[threadIdx.x] = oi; }
+        }
+        __syncthreads();
+    }
+    bv_out = rv[0];
+    bi_out = ri[0] == n ? 0 : ri[0];
+}
+
+// InterleavedRoPE::new tables (crates/tang-compute/src/modules.rs:495-511):
+// freq = 1/base^(i/half), angle = pos*freq in f64, stored f32.
+inline void rope_tables_host(size_t head_dim, size_t max_seq, double base, float* cs, float* sn) {
+    const size_t half = head_dim / 2;
+    for (size_t pos = 0; pos < max_seq; pos++) {
+        for (size_t i = 0; i < half; i++) {
+            const double freq = 1.0 / std::pow(base, (double)i / (double)half);
+            const double angle = (double)pos * freq;
+            cs[pos * half + i] = (float)std::cos(angle);
+            sn[pos * half + i] = (float)std::sin(angle);
+        }
+    }
+}
+
+}  // namespace th

@@ -1,0 +1,173 @@
+// Launchers and C entry points for the quantized linear kernels.
+#include "capi_util.hpp"
+#include "qlinear.hpp"
+
+namespace th {
+
+template <typename K>
+static void set_smem(K kernel, size_t bytes) {
+    if (bytes > 48 * 1024)
+        TH_HIP(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+}
+
+template <int M, bool XF32, typename ST>
+static void q4_gemv_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy,
+                           hipStream_t s) {
+    const size_t smem = Q4GemvSmem<M, XF32>::bytes((int)w->Kp);
+    TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
+    auto k = q4_gemv_kernel<M, XF32, ST, EpiStore>;
+    set_smem(k, smem);
+    EpiStore epi{y, (int)ldy};
+    hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
+                       (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi);
+    TH_LAUNCH_CHECK();
+}
+
+template <bool XF32, typename ST>
+static void q4_gemv_dispatch(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y,
+                             size_t ldy, hipStream_t s) {
+    switch (m) {
+        case 1: q4_gemv_launch<1, XF32, ST>(w, x, ldx, y, ldy, s); break;
+        case 2: q4_gemv_launch<2, XF32, ST>(w, x, ldx, y, ldy, s); break;
+        case 3: q4_gemv_launch<3, XF32, ST>(w, x, ldx, y, ldy, s); break;
+        case 4: q4_gemv_launch<4, XF32, ST>(w, x, ldx, y, ldy, s); break;
+        default: throw Error(TH_ERR_INVALID, "q4 gemv: m out of range");
+    }
+}
+
+// Sum KS split-K partials [KS][m][ldy] in split order.
+__global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N,
+                                     int ldy, int KS) {
+    const size_t total = (size_t)M * N;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t m = i / N, n = i - m * N;
+        float v = 0.0f;
+        for (int s = 0; s < KS; s++) v += part[((size_t)s * M + m) * N + n];
+        y[m * ldy + n] = v;
+    }
+}
+
+template <int RT, int CB, bool XF32, typename ST>
+static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
+                           hipStream_t s, th_device* dev) {
+    const size_t NT = w->Np / 16, GQ = w->Kp / 128;
+    const unsigned gx = (unsigned)ceil_div(NT, 4 * RT);
+    const unsigned gy = (unsigned)ceil_div(m, 16 * CB);
+    // Split K so that the grid covers the chip at least twice.
+    const size_t target = 2 * (size_t)(dev ? dev->num_cus : 256);
+    size_t ks = 1;
+    while ((size_t)gx * gy * ks < target && ks * 2 <= GQ && ks < 16) ks *= 2;
+    const int gps = (int)ceil_div(GQ, ks);
+    ks = ceil_div(GQ, (size_t)gps);
+    float* out = y;
+    int ldo = (int)ldy;
+    if (ks > 1) {
+        out = (float*)device_scratch(dev, ks * m * w->rows * sizeof(float));
+        ldo = (int)w->rows;
+    }
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<RT, CB, XF32, ST>), dim3(gx, gy, (unsigned)ks), dim3(256), 0, s,
+                       (const uint4*)w->data, (const ST*)w->scales, x, out, (int)m, (int)w->rows,
+                       (int)w->cols, (int)w->Kp, (int)ldx, ldo, gps);
+    TH_LAUNCH_CHECK();
+    if (ks > 1) {
+        const size_t total = m * w->rows;
+        unsigned blocks = (unsigned)std::min<size_t>(ceil_div(total, 256), 4096);
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, out, y, (int)m, (int)w->rows,
+                           (int)ldy, (int)ks);
+        TH_LAUNCH_CHECK();
+    }
+}
+
+template <bool XF32, typename ST>
+static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
+                        hipStream_t s, th_device* dev) {
+    if (m <= 4) q4_gemv_dispatch<XF32, ST>(w, x, m, ldx, y, ldy, s);
+    else if (m <= 16) q4_mfma_launch<1, 1, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
+    else q4_mfma_launch<2, 4, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
+}
+
+void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
+                      size_t ldy, hipStream_t s, th_device* dev) {
+    TH_REQUIRE(w && w->bits == 4, "not a q4 weight");
+    TH_REQUIRE(xdt == TH_F32 || xdt == TH_BF16, "activations must be f32 or bf16");
+    if (m == 0) return;
+    const bool f32 = xdt == TH_F32;
+    if (w->scale_dtype == TH_F16) {
+        if (f32) q4_linear_t<true, _Float16>(w, x, m, ldx, y, ldy, s, dev);
+        else q4_linear_t<false, _Float16>(w, x, m, ldx, y, ldy, s, dev);
+    } else {
+        if (f32) q4_linear_t<true, float>(w, x, m, ldx, y, ldy, s, dev);
+        else q4_linear_t<false, float>(w, x, m, ldx, y, ldy, s, dev);
+    }
+}
+
+template <int M, bool XF32, bool PR>
+static void q8_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
+    const size_t smem = Q8GemvSmem<M>::bytes((int)w->Kp);
+    TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
+    auto k = q8_gemv_kernel<M, XF32, PR, EpiStore>;
+    set_smem(k, smem);
+    EpiStore epi{y, (int)ldy};
+    hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
+                       (const float*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi);
+    TH_LAUNCH_CHECK();
+}
+
+template <bool XF32, bool PR>
+static void q8_dispatch(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
+                        hipStream_t s) {
+    // Process up to 4 activation rows per launch.
+    for (size_t m0 = 0; m0 < m; m0 += 4) {
+        const size_t mm = std::min<size_t>(4, m - m0);
+        const void* xo = (const char*)x + m0 * ldx * (XF32 ? 4 : 2);
+        float* yo = y + m0 * ldy;
+        switch (mm) {
+            case 1: q8_launch<1, XF32, PR>(w, xo, ldx, yo, ldy, s); break;
+            case 2: q8_launch<2, XF32, PR>(w, xo, ldx, yo, ldy, s); break;
+            case 3: q8_launch<3, XF32, PR>(w, xo, ldx, yo, ldy, s); break;
+            default: q8_launch<4, XF32, PR>(w, xo, ldx, yo, ldy, s); break;
+        }
+    }
+}
+
+void launch_q8_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
+                      size_t ldy, hipStream_t s) {
+    TH_REQUIRE(w && w->bits == 8, "not a q8 weight");
+    TH_REQUIRE(xdt == TH_F32 || xdt == TH_BF16, "activations must be f32 or bf16");
+    if (m == 0) return;
+    if (xdt == TH_F32) {
+        if (w->per_row) q8_dispatch<true, true>(w, x, m, ldx, y, ldy, s);
+        else q8_dispatch<true, false>(w, x, m, ldx, y, ldy, s);
+    } else {
+        if (w->per_row) q8_dispatch<false, true>(w, x, m, ldx, y, ldy, s);
+        else q8_dispatch<false, false>(w, x, m, ldx, y, ldy, s);
+    }
+}
+
+}  // namespace th
+
+using namespace th;
+
+extern "C" {
+
+int th_gemm_q4(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y) {
+    TH_API_BEGIN
+    TH_REQUIRE(dev && x && w && y, "null argument");
+    TH_REQUIRE(w->bits == 4, "weight is not q4");
+    require_len_any(x, m * w->cols, "x");
+    require_len(y, TH_F32, m * w->rows, "y");
+    launch_q4_linear(w, x->ptr, x->dtype, m, w->cols, (float*)y->ptr, w->rows, dev->stream, dev);
+    TH_API_END
+}
+
+int th_gemv_q8(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y) {
+    TH_API_BEGIN
+    TH_REQUIRE(dev && x && w && y, "null argument");
+    TH_REQUIRE(w->bits == 8, "weight is not q8");
+    require_len_any(x, m * w->cols, "x");
+    require_len(y, TH_F32, m * w->rows, "y");
+    launch_q8_linear(w, x->ptr, x->dtype, m, w->cols, (float*)y->ptr, w->rows, dev->stream);
+    TH_API_END
+}
+
+}  // extern "C"
