@@ -122,6 +122,15 @@ int th_qweight_free(th_qweight* w);
 int th_gemm_q4(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y);
 int th_gemv_q8(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y);
 
+/* Benchmark helper (no reference counterpart): enqueue `iters` calls of
+ * th_gemm_q4 / th_gemv_q8 (by the weights' bit width) on x -> y, cycling
+ * through the n_w weights (all of one shape) so the streamed bytes exceed the
+ * last-level cache, and return the elapsed milliseconds between HIP events
+ * recorded on the device stream around them.  use_graph != 0 captures the
+ * calls into one HIP graph first and times its replay. */
+int th_bench_linear(th_device* dev, const th_buffer* x, size_t m, th_qweight* const* ws, size_t n_w,
+                    th_buffer* y, size_t iters, int use_graph, float* ms);
+
 /* ---- decode ops (f32 buffers unless stated) ---------------------------- */
 
 /* CpuDevice::rms_norm (crates/tang-compute/src/cpu.rs:126); weight f32 or bf16. */

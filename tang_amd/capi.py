@@ -68,6 +68,7 @@ SIGNATURES = {
     "th_qweight_free": ([_P], _I),
     "th_gemm_q4": ([_P, _P, _S, _P, _P], _I),
     "th_gemv_q8": ([_P, _P, _S, _P, _P], _I),
+    "th_bench_linear": ([_P, _P, _S, _P, _S, _P, _S, _I, _P], _I),
     "th_rms_norm": ([_P, _P, _P, _S, _S, _F, _P], _I),
     "th_rms_norm_residual": ([_P, _P, _P, _P, _S, _S, _F, _P, _P], _I),
     "th_rope_tables": ([_S, _S, _D, _P, _P], _I),
@@ -312,6 +313,14 @@ class HipComputeDevice:
         y = y or self.alloc(m * w.rows)
         check(lib().th_gemv_q8(self.handle, x.handle, m, w.handle, y.handle))
         return y
+
+    def bench_linear(self, x, m, weights, y, iters, use_graph=False):
+        """Elapsed ms of `iters` quantized linears cycling through `weights`."""
+        arr = (ctypes.c_void_p * len(weights))(*[w.handle.value for w in weights])
+        ms = ctypes.c_float()
+        check(lib().th_bench_linear(self.handle, x.handle, m, arr, len(weights), y.handle, iters,
+                                    1 if use_graph else 0, ctypes.byref(ms)))
+        return ms.value
 
     # -- decode ops
     def rms_norm(self, data, weight, n_groups, dim, eps):

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "capi_util.hpp"
+#include "qlinear.hpp"
 
 namespace th {
 
@@ -62,16 +63,26 @@ th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_d
     const size_t GQ = Kp / 128, NT = Np / 16;
     std::vector<uint8_t> tiles(NT * GQ * 1024, 0x88);
     const size_t ssz = dtype_size(sdt);
-    std::vector<uint8_t> stile(NT * GQ * 64 * ssz, 0);
+    const bool f16 = sdt == TH_F16;
+    std::vector<uint8_t> stile(q4_scale_count(f16, NT, GQ) * ssz, 0);
     for (size_t row = 0; row < rows; row++) {
         const size_t t = row / 16, rr = row % 16;
         for (size_t g = 0; g < bpr; g++) {
             const size_t gq = g / 4, j = g % 4;
             const uint8_t* src = nib + (row * bpr + g) * 16;
+            uint8_t tail[16];
+            if (g == bpr - 1 && cols % 32) {
+                // Elements past `cols` are ignored by q4_matvec (quantize.rs:277-282):
+                // store them as the zero code so the kernels may read any finite x there.
+                std::memcpy(tail, src, 16);
+                for (size_t e = cols % 32; e < 32; e++)
+                    tail[e / 2] = (e & 1) ? (uint8_t)((tail[e / 2] & 0x0F) | 0x80) : (uint8_t)((tail[e / 2] & 0xF0) | 0x08);
+                src = tail;
+            }
             uint8_t* tb = tiles.data() + (t * GQ + gq) * 1024;
             for (size_t q = 0; q < 4; q++) std::memcpy(tb + (q * 16 + rr) * 16 + j * 4, src + q * 4, 4);
             const uint8_t* s = (const uint8_t*)scales + (row * bpr + g) * ssz;
-            std::memcpy(stile.data() + (((t * GQ + gq) * 16 + rr) * 4 + j) * ssz, s, ssz);
+            std::memcpy(stile.data() + q4_scale_index(f16, t, gq, rr, j, GQ) * ssz, s, ssz);
         }
     }
     th_qweight* w = new th_qweight();
@@ -107,7 +118,7 @@ void q4_unpack(const th_qweight* w, th_q4_block* out) {
             th_q4_block& b = out[row * bpr + g];
             const uint8_t* tb = tiles.data() + (t * GQ + gq) * 1024;
             for (size_t q = 0; q < 4; q++) std::memcpy(b.values + q * 4, tb + (q * 16 + rr) * 16 + j * 4, 4);
-            const uint8_t* s = stile.data() + (((t * GQ + gq) * 16 + rr) * 4 + j) * ssz;
+            const uint8_t* s = stile.data() + q4_scale_index(w->scale_dtype == TH_F16, t, gq, rr, j, GQ) * ssz;
             if (w->scale_dtype == TH_F32) std::memcpy(&b.scale, s, 4);
             else { uint16_t h; std::memcpy(&h, s, 2); b.scale = f16_to_f32_host(h); }
         }

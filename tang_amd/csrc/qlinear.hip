@@ -1,26 +1,48 @@
 // Launchers and C entry points for the quantized linear kernels.
+#include <map>
+#include <mutex>
+
 #include "capi_util.hpp"
 #include "qlinear.hpp"
 
 namespace th {
 
+// Raise a kernel's dynamic-LDS limit (once per kernel and size).
 template <typename K>
 static void set_smem(K kernel, size_t bytes) {
-    if (bytes > 48 * 1024)
+    static std::mutex mu;
+    static std::map<const void*, size_t> done;
+    if (bytes <= 48 * 1024) return;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& d = done[(const void*)kernel];
+    if (bytes > d) {
         TH_HIP(hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+        d = bytes;
+    }
 }
 
-template <int M, bool XF32, typename ST>
-static void q4_gemv_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy,
-                           hipStream_t s) {
-    const size_t smem = Q4GemvSmem<M, XF32>::bytes((int)w->Kp);
+// Vector activation loads need K, the row stride and the base 16-byte aligned.
+static bool x_vec_ok(const void* x, size_t ldx, size_t K) {
+    return K % 8 == 0 && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0;
+}
+
+template <int M, bool XF32, typename ST, bool VEC>
+static void q4_gemv_launch_v(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
+    constexpr int MR = XF32 ? 2 * M : M;
+    const size_t smem = Q4GemvSmem<MR>::bytes((int)(w->Kp / 128));
     TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
-    auto k = q4_gemv_kernel<M, XF32, ST, EpiStore>;
+    auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore>;
     set_smem(k, smem);
     EpiStore epi{y, (int)ldy};
     hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
                        (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi);
     TH_LAUNCH_CHECK();
+}
+
+template <int M, bool XF32, typename ST>
+static void q4_gemv_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
+    if (x_vec_ok(x, ldx, w->cols)) q4_gemv_launch_v<M, XF32, ST, true>(w, x, ldx, y, ldy, s);
+    else q4_gemv_launch_v<M, XF32, ST, false>(w, x, ldx, y, ldy, s);
 }
 
 template <bool XF32, typename ST>
@@ -101,16 +123,22 @@ void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m
     }
 }
 
-template <int M, bool XF32, bool PR>
-static void q8_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
+template <int M, bool XF32, bool PR, bool VEC>
+static void q8_launch_v(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
     const size_t smem = Q8GemvSmem<M>::bytes((int)w->Kp);
     TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
-    auto k = q8_gemv_kernel<M, XF32, PR, EpiStore>;
+    auto k = q8_gemv_kernel<M, XF32, VEC, PR, EpiStore>;
     set_smem(k, smem);
     EpiStore epi{y, (int)ldy};
     hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
                        (const float*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi);
     TH_LAUNCH_CHECK();
+}
+
+template <int M, bool XF32, bool PR>
+static void q8_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
+    if (x_vec_ok(x, ldx, w->cols)) q8_launch_v<M, XF32, PR, true>(w, x, ldx, y, ldy, s);
+    else q8_launch_v<M, XF32, PR, false>(w, x, ldx, y, ldy, s);
 }
 
 template <bool XF32, bool PR>
@@ -167,6 +195,48 @@ int th_gemv_q8(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w
     require_len_any(x, m * w->cols, "x");
     require_len(y, TH_F32, m * w->rows, "y");
     launch_q8_linear(w, x->ptr, x->dtype, m, w->cols, (float*)y->ptr, w->rows, dev->stream);
+    TH_API_END
+}
+
+int th_bench_linear(th_device* dev, const th_buffer* x, size_t m, th_qweight* const* ws, size_t n_w, th_buffer* y,
+                    size_t iters, int use_graph, float* ms) {
+    TH_API_BEGIN
+    TH_REQUIRE(dev && x && ws && n_w > 0 && y && ms, "null argument");
+    const th_qweight* w0 = ws[0];
+    for (size_t i = 0; i < n_w; i++)
+        TH_REQUIRE(ws[i] && ws[i]->bits == w0->bits && ws[i]->rows == w0->rows && ws[i]->cols == w0->cols,
+                   "weights must share one shape");
+    require_len_any(x, m * w0->cols, "x");
+    require_len(y, TH_F32, m * w0->rows, "y");
+    auto call = [&](size_t i) {
+        const th_qweight* w = ws[i % n_w];
+        if (w->bits == 4) launch_q4_linear(w, x->ptr, x->dtype, m, w->cols, (float*)y->ptr, w->rows, dev->stream, dev);
+        else launch_q8_linear(w, x->ptr, x->dtype, m, w->cols, (float*)y->ptr, w->rows, dev->stream);
+    };
+    call(0);  // sizes the workspace before any capture
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    if (use_graph) {
+        hipGraph_t g;
+        hipGraphExec_t ge;
+        TH_HIP(hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal));
+        for (size_t i = 0; i < iters; i++) call(i);
+        TH_HIP(hipStreamEndCapture(dev->stream, &g));
+        TH_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        TH_HIP(hipGraphLaunch(ge, dev->stream));  // warm replay
+        TH_HIP(hipEventRecord(dev->ev_start, dev->stream));
+        TH_HIP(hipGraphLaunch(ge, dev->stream));
+        TH_HIP(hipEventRecord(dev->ev_stop, dev->stream));
+        TH_HIP(hipEventSynchronize(dev->ev_stop));
+        TH_HIP(hipGraphExecDestroy(ge));
+        TH_HIP(hipGraphDestroy(g));
+    } else {
+        for (size_t i = 0; i < n_w; i++) call(i);
+        TH_HIP(hipEventRecord(dev->ev_start, dev->stream));
+        for (size_t i = 0; i < iters; i++) call(i);
+        TH_HIP(hipEventRecord(dev->ev_stop, dev->stream));
+        TH_HIP(hipEventSynchronize(dev->ev_stop));
+    }
+    TH_HIP(hipEventElapsedTime(ms, dev->ev_start, dev->ev_stop));
     TH_API_END
 }
 

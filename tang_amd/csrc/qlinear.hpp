@@ -7,6 +7,8 @@
 // Weight layouts are described next to th_qweight in common.hpp.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace th {
@@ -37,11 +39,24 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 // Four nibble pairs of one packed word as bf16 pairs holding 128+nibble:
 // pair k = (element k, element k+4) of the word's eight elements.  bf16 with
 // exponent 2^7 has unit spacing, so 0x4300|n is exactly 128+n.
-__device__ __forceinline__ void nib_pairs_bf16(uint32_t w, uint32_t p[4]) {
-    p[0] = (w & 0x000F000Fu) | 0x43004300u;
-    p[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-    p[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-    p[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+// The eight nibbles of one packed word (reference order: byte b holds
+// elements 2b (low nibble) and 2b+1 (high nibble)) as four bf16 pairs of
+// 128+nibble, built with byte permutes: lo/hi = the low/high nibbles of the
+// four bytes, then v_perm_b32 splices in the 0x43 high bytes.
+// Pair order: (e0,e2), (e4,e6), (e1,e3), (e5,e7); pack_x_q4 matches it.
+__device__ __forceinline__ void nib_pairs_perm(uint32_t w, uint32_t p[4]) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+    const uint32_t c43 = 0x43434343u;
+    p[0] = __builtin_amdgcn_perm(c43, lo, 0x04010400u);
+    p[1] = __builtin_amdgcn_perm(c43, lo, 0x04030402u);
+    p[2] = __builtin_amdgcn_perm(c43, hi, 0x04010400u);
+    p[3] = __builtin_amdgcn_perm(c43, hi, 0x04030402u);
+}
+
+// Eight bf16 x values as the pairs nib_pairs_perm produces.
+__device__ __forceinline__ uint4 pack_x_q4(const uint32_t h[8]) {
+    return make_uint4(h[0] | (h[2] << 16), h[4] | (h[6] << 16), h[1] | (h[3] << 16), h[5] | (h[7] << 16));
 }
 
 // Eight x values x[0..8) as the matching bf16 pairs (x0,x4),(x1,x5),(x2,x6),(x3,x7).
@@ -87,14 +102,6 @@ struct EpiStore {
 // and both halves are dotted.
 // ---------------------------------------------------------------------------
 
-template <int M, bool XF32>
-struct Q4GemvSmem {
-    static constexpr int XR = XF32 ? 2 * M : M;
-    static size_t bytes(int Kp) {
-        return (size_t)XR * (Kp / 8) * 16 + (size_t)M * (Kp / 8) * 4 + 4 * 16 * M * 4;
-    }
-};
-
 template <int U, typename ST>
 struct ScaleVec;
 template <int U>
@@ -116,159 +123,299 @@ struct ScaleVec<U, float> {
     }
 };
 
-template <int M, bool XF32, typename ST, typename Epi>
-__global__ __launch_bounds__(256) void q4_gemv_kernel(const uint4* __restrict__ wt,
+// Eight consecutive activations x[m][k0..k0+8) of one row, raw: bf16 in
+// a.xyzw, or f32 in a (elements 0-3) and b (4-7).  Elements at k >= K read as
+// zero (VEC: finite values whose weights are zero).  Branch-free, so the
+// loads stay in flight alongside the weight stream.  VEC requires K % 8 == 0,
+// ldx % 8 == 0 and a 16-byte aligned base.
+template <bool XF32, bool VEC>
+__device__ __forceinline__ void load_x8(const void* xin, int m, int ldx, int K, int k0, uint4& a, uint4& b) {
+    if (VEC) {
+        // Chunks past K re-read the row start: the weights there are exact
+        // zeros (packing forces elements >= K to the zero code), so any
+        // finite value contributes nothing.
+        const int kk = k0 < K ? k0 : 0;
+        if (XF32) {
+            const float* xr = (const float*)xin + (size_t)m * ldx + kk;
+            a = *(const uint4*)xr;
+            b = *(const uint4*)(xr + 4);
+        } else {
+            const uint16_t* xr = (const uint16_t*)xin + (size_t)m * ldx + kk;
+            a = *(const uint4*)xr;
+            b = make_uint4(0, 0, 0, 0);
+        }
+    } else {
+        uint32_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int k = k0 + i;
+            const int kk = k < K ? k : 0;
+            uint32_t t = XF32 ? __float_as_uint(((const float*)xin)[(size_t)m * ldx + kk])
+                              : (uint32_t)((const uint16_t*)xin)[(size_t)m * ldx + kk];
+            v[i] = k < K ? t : 0u;
+        }
+        if (XF32) {
+            a = make_uint4(v[0], v[1], v[2], v[3]);
+            b = make_uint4(v[4], v[5], v[6], v[7]);
+        } else {
+            a = make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16), v[6] | (v[7] << 16));
+            b = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+// Index of scale (row-tile t, group-quad gq, row r, group-in-quad j) in the
+// q4 scale array.  f16: pairs of group-quads gq, gq+4 that one wave streams
+// back to back sit in one 16-byte record per row:
+//   [t][gq/8][gq%4][r][(gq%8)/4][j]   (GQ8 = ceil(GQ/8) octets per tile)
+// f32: [t][gq][r][j].
+__host__ __device__ inline size_t q4_scale_index(bool f16, size_t t, size_t gq, size_t r, size_t j, size_t GQ) {
+    if (f16) {
+        const size_t GQ8 = (GQ + 7) / 8;
+        return ((((t * GQ8 + gq / 8) * 4 + gq % 4) * 16 + r) * 2 + (gq % 8) / 4) * 4 + j;
+    }
+    return ((t * GQ + gq) * 16 + r) * 4 + j;
+}
+inline size_t q4_scale_count(bool f16, size_t NT, size_t GQ) {
+    return f16 ? NT * ((GQ + 7) / 8) * 512 : NT * GQ * 64;
+}
+
+// LDS bytes of the MFMA GEMV: per wave, x as [item][j][MR][q] 16-byte
+// chunks plus a zero chunk, and the bias as [item][j][8] floats.
+template <int MR>
+struct Q4GemvSmem {
+    __host__ __device__ static size_t per_wave(int items) { return (size_t)items * 4 * (MR * 64 + 32) + 16; }
+    static size_t bytes(int GQ) {
+        const int items = (GQ + 3) / 4;
+        return 4 * per_wave(items) + 4 * 8 * 16 * 4;
+    }
+};
+
+// Scale access for one 16-byte scale record per lane: f16 holds two items
+// (u even/odd halves), f32 one item.
+template <typename ST>
+struct ScaleRec;
+template <>
+struct ScaleRec<_Float16> {
+    static constexpr int ITEMS = 2;
+    __device__ __forceinline__ static float get(const uint4& v, int h, int j) {
+        const uint32_t w = h ? (j < 2 ? v.z : v.w) : (j < 2 ? v.x : v.y);
+        const uint16_t b = (j & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFF);
+        return (float)__builtin_bit_cast(_Float16, b);
+    }
+};
+template <>
+struct ScaleRec<float> {
+    static constexpr int ITEMS = 1;
+    __device__ __forceinline__ static float get(const uint4& v, int, int j) {
+        return __uint_as_float(j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w);
+    }
+};
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------
+// int4 GEMV for m <= 4 on MFMA, "transposed": A = activations (row m = batch
+// row, MR rows used: m, or hi/lo bf16 halves 2m, 2m+1 for f32 input),
+// B = the tile's weights (column n = weight row).  One
+// v_mfma_f32_16x16x32_bf16 per group of 32: B holds 128+nibble as bf16
+// (exact), C carries bias = -136 * sum(x over the group) so
+// D[m][n] = sum (nibble-8) * x, and acc[m][n] += scale[n][g] * D[m][n].
+// One workgroup = one 16-row tile; wave w takes group-quads gq = w + 4i
+// ("items"), stages only the activations it needs in its own LDS region
+// (no workgroup barrier) and keeps D group-quads of weights in flight.
+// ---------------------------------------------------------------------------
+template <int MR, bool XF32, bool VEC, typename ST, typename Epi>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR <= 1 ? 4 : 2))) void q4_gemv_kernel(const uint4* __restrict__ wt,
                                                       const ST* __restrict__ sc,
                                                       const void* __restrict__ xin, int K, int Kp,
                                                       int N, int ldx, Epi epi) {
-    constexpr int XR = XF32 ? 2 * M : M;
-    constexpr int U = 4;  // group-quads in flight per wave
+    constexpr int D = 8;          // items in flight per wave (rolling prefetch)
+    constexpr int SI = ScaleRec<ST>::ITEMS;
+    constexpr int NS = D / SI;    // scale records in flight
+    constexpr int M = XF32 ? MR / 2 : MR;  // activation rows
+    constexpr bool F16S = std::is_same<ST, _Float16>::value;
     extern __shared__ uint4 smem[];
     const int GQ = Kp >> 7;
-    const int NC = Kp >> 3;  // 8-element chunks per x row
-    uint4* xl = smem;                                        // [XR][NC]
-    float* bias = (float*)(xl + (size_t)XR * NC);            // [M][NC]
-    float* red = bias + (size_t)M * NC;                      // [4][M][16]
+    const int items_max = (GQ + 3) >> 2;
 
     const int t = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
-    const int nmine = (GQ - wave + 3) >> 2;  // group-quads of this wave
+    const int nmine = (GQ - wave + 3) >> 2;  // items of this wave (wave-uniform)
+
+    // per-wave LDS region
+    char* wl = (char*)smem + (size_t)wave * Q4GemvSmem<MR>::per_wave(items_max);
+    uint4* xw = (uint4*)wl;                                   // [item][j][MR][4]
+    uint4* zero = xw + (size_t)items_max * 4 * MR * 4;        // one zero chunk
+    float* bw = (float*)(zero + 1);                           // [item][j][8]
+    float* red = (float*)((char*)smem + 4 * Q4GemvSmem<MR>::per_wave(items_max));  // [4][8][16]
+
     const uint4* wp = wt + (size_t)t * GQ * 64 + lane;
-    const ST* sp = sc + (size_t)t * GQ * 64 + r * 4;
+    auto item_off = [&](int i) { return (size_t)(i < nmine ? wave + 4 * i : 0) * 64; };
+    auto scale_ptr = [&](int i) -> const uint4* {
+        const int gq = i < nmine ? wave + 4 * i : 0;  // past the end: a valid record of this tile
+        return (const uint4*)(sc + q4_scale_index(F16S, t, F16S ? (gq & ~4) : gq, r, 0, GQ));
+    };
 
-    // First batch of weights in flight before x is staged.
-    uint4 wcur[U];
-    ScaleVec<U, ST> scur;
+    // 1. activations for this wave's groups: task (item i, group j, row m)
+    //    covers 32 values (4 chunks); a lane takes up to TPL tasks.
+    constexpr int TPL = 2;
+    const int ntask = nmine * 4 * M;
+    uint4 xa[TPL][4], xb[TPL][4];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        int gq = wave + 4 * u;
-        if (u < nmine) {
-            wcur[u] = ldg_stream(wp + (size_t)gq * 64);
-            scur.load(sp + (size_t)gq * 64, u);
-        }
+    for (int tt = 0; tt < TPL; tt++) {
+        int task = lane + tt * 64;
+        task = task < ntask ? task : 0;
+        const int m = task % M, ij = task / M, i = ij >> 2, j = ij & 3;
+        const int g = 4 * (wave + 4 * i) + j;
+#pragma unroll
+        for (int c = 0; c < 4; c++) load_x8<XF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, xa[tt][c], xb[tt][c]);
     }
-
-    // Stage x (vector loads only when every row start is 16-byte aligned).
-    const bool vec = (ldx & 7) == 0 && (((uintptr_t)xin) & 15) == 0;
-    for (int c = tid; c < M * NC; c += 256) {
-        const int m = c / NC, cc = c - m * NC;
-        const int k0 = cc * 8;
-        float xv[8];
-        if (XF32) {
-            const float* xr = (const float*)xin + (size_t)m * ldx;
-            if (vec && k0 + 8 <= K) {
-                float4 a = *(const float4*)(xr + k0), b = *(const float4*)(xr + k0 + 4);
-                xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-                xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
-            } else {
+    // 2. weights and scales in flight
+    uint4 wbuf[D], sbuf[NS];
 #pragma unroll
-                for (int i = 0; i < 8; i++) xv[i] = (k0 + i < K) ? xr[k0 + i] : 0.0f;
-            }
-        } else {
-            const uint16_t* xr = (const uint16_t*)xin + (size_t)m * ldx;
-            if (vec && k0 + 8 <= K) {
-                uint4 a = *(const uint4*)(xr + k0);
-                uint32_t w4[4] = {a.x, a.y, a.z, a.w};
+    for (int u = 0; u < D; u++) wbuf[u] = ldg_stream(wp + item_off(u));
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    xv[2 * i] = bf16_bits_to_f32(w4[i] & 0xFFFF);
-                    xv[2 * i + 1] = bf16_bits_to_f32(w4[i] >> 16);
-                }
-            } else {
+    for (int v = 0; v < NS; v++) sbuf[v] = *scale_ptr(v * SI);
+    // 3. stage: bf16 pairs in nibble-pair order; f32 input as hi/lo rows
+    auto stage = [&](int task, const uint4* ra, const uint4* rb) {
+        const int m = task % M, ij = task / M;
+        float s_hi = 0.0f, s_lo = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 8; i++) xv[i] = (k0 + i < K) ? bf16_bits_to_f32(xr[k0 + i]) : 0.0f;
-            }
-        }
-        uint32_t hi[8], lo[8];
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            hi[i] = XF32 ? f32_to_bf16_bits(xv[i]) : f32_to_bf16_bits(xv[i]);
-            float fh = bf16_bits_to_f32(hi[i]);
-            s += fh;
+        for (int c = 0; c < 4; c++) {
+            float xv[8];
             if (XF32) {
-                lo[i] = f32_to_bf16_bits(xv[i] - fh);
-                s += bf16_bits_to_f32(lo[i]);
+                xv[0] = __uint_as_float(ra[c].x); xv[1] = __uint_as_float(ra[c].y);
+                xv[2] = __uint_as_float(ra[c].z); xv[3] = __uint_as_float(ra[c].w);
+                xv[4] = __uint_as_float(rb[c].x); xv[5] = __uint_as_float(rb[c].y);
+                xv[6] = __uint_as_float(rb[c].z); xv[7] = __uint_as_float(rb[c].w);
+            } else {
+                const uint32_t w4[4] = {ra[c].x, ra[c].y, ra[c].z, ra[c].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
+                    xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
+                }
+            }
+            uint32_t hi[8], lo[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                hi[e] = f32_to_bf16_bits(xv[e]);
+                const float fh = bf16_bits_to_f32(hi[e]);
+                s_hi += fh;
+                if (XF32) {
+                    lo[e] = f32_to_bf16_bits(xv[e] - fh);
+                    s_lo += bf16_bits_to_f32(lo[e]);
+                }
+            }
+            if (XF32) {
+                xw[((size_t)ij * MR + 2 * m) * 4 + c] = pack_x_q4(hi);
+                xw[((size_t)ij * MR + 2 * m + 1) * 4 + c] = pack_x_q4(lo);
+            } else {
+                xw[((size_t)ij * MR + m) * 4 + c] = pack_x_q4(hi);
             }
         }
         if (XF32) {
-            xl[(size_t)(2 * m) * NC + cc] = pack_perm_bf16(hi);
-            xl[(size_t)(2 * m + 1) * NC + cc] = pack_perm_bf16(lo);
+            bw[ij * 8 + 2 * m] = -136.0f * s_hi;
+            bw[ij * 8 + 2 * m + 1] = -136.0f * s_lo;
         } else {
-            xl[(size_t)m * NC + cc] = pack_perm_bf16(hi);
+            bw[ij * 8 + m] = -136.0f * s_hi;
         }
-        // chunk cc = group g (= 4gq + j), lane-quad qq; bias index (gq*4 + qq)*4 + j
-        const int g = cc >> 2, qq = cc & 3, gq = g >> 2, j = g & 3;
-        bias[(size_t)m * NC + (gq * 4 + qq) * 4 + j] = -136.0f * s;
+    };
+    if (lane == 0) *zero = make_uint4(0, 0, 0, 0);
+    for (int ij = lane; ij < nmine * 4; ij += 64)
+        for (int e = MR; e < 8; e++) bw[ij * 8 + e] = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < TPL; tt++) {
+        const int task = lane + tt * 64;
+        if (task < ntask) stage(task, xa[tt], xb[tt]);
     }
-    __syncthreads();
-
-    float acc[M];
+    for (int task = lane + TPL * 64; task < ntask; task += 64) {
+        uint4 ra[4], rb[4];
+        const int m = task % M, ij = task / M, i = ij >> 2, j = ij & 3;
+        const int g = 4 * (wave + 4 * i) + j;
 #pragma unroll
-    for (int m = 0; m < M; m++) acc[m] = 0.0f;
-
-    for (int base = 0; base < nmine; base += U) {
-        uint4 wnxt[U];
-        ScaleVec<U, ST> snxt;
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            int i = base + U + u;
-            if (i < nmine) {
-                int gq = wave + 4 * i;
-                wnxt[u] = ldg_stream(wp + (size_t)gq * 64);
-                snxt.load(sp + (size_t)gq * 64, u);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            int i = base + u;
-            if (i < nmine) {
-                const int gq = wave + 4 * i;
-                const uint32_t wv[4] = {wcur[u].x, wcur[u].y, wcur[u].z, wcur[u].w};
-#pragma unroll
-                for (int m = 0; m < M; m++) {
-                    const float4 b4 = *(const float4*)(bias + (size_t)m * NC + (gq * 4 + q) * 4);
-                    const float bj[4] = {b4.x, b4.y, b4.z, b4.w};
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        uint32_t p[4];
-                        nib_pairs_bf16(wv[j], p);
-                        const int cidx = (4 * gq + j) * 4 + q;
-                        float d = bj[j];
-                        const uint4 xa = xl[(size_t)(XF32 ? 2 * m : m) * NC + cidx];
-                        d = dot2_bf16(p[0], xa.x, d);
-                        d = dot2_bf16(p[1], xa.y, d);
-                        d = dot2_bf16(p[2], xa.z, d);
-                        d = dot2_bf16(p[3], xa.w, d);
-                        if (XF32) {
-                            const uint4 xb = xl[(size_t)(2 * m + 1) * NC + cidx];
-                            d = dot2_bf16(p[0], xb.x, d);
-                            d = dot2_bf16(p[1], xb.y, d);
-                            d = dot2_bf16(p[2], xb.z, d);
-                            d = dot2_bf16(p[3], xb.w, d);
-                        }
-                        acc[m] = __builtin_fmaf(scur.get(u, j), d, acc[m]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) wcur[u] = wnxt[u];
-        scur = snxt;
+        for (int c = 0; c < 4; c++) load_x8<XF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, ra[c], rb[c]);
+        stage(task, ra, rb);
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int ACC = MR < 4 ? MR : 4;
+    // A rows >= MR and C rows >= MR only feed D rows that are discarded, so
+    // those lanes read real (finite) data of another row: no masking needed.
+    const uint4* abase = xw + (size_t)(r < MR ? r : 0) * 4 + q;
+    const float* cbase = bw + 4 * (q & 1);
+    float4_t dprev = {0.0f, 0.0f, 0.0f, 0.0f};
+    float sprev = 0.0f;
+
+    auto step = [&](auto refill_tag, int u, int i) {
+        const bool valid = i < nmine;
+        const int ii = valid ? i : 0;
+        const uint4 wv = wbuf[u];
+        const uint4 sv = sbuf[u / SI];
+        float sj[4];
 #pragma unroll
-    for (int m = 0; m < M; m++) {
-        float v = wave_sum_xor16_32(acc[m]);
-        if (q == 0) red[(wave * M + m) * 16 + r] = v;
+        for (int j = 0; j < 4; j++) sj[j] = valid ? ScaleRec<ST>::get(sv, u % SI, j) : 0.0f;
+        if constexpr (decltype(refill_tag)::value) {
+            wbuf[u] = ldg_stream(wp + item_off(i + D));
+            if (u % SI == SI - 1) sbuf[u / SI] = *scale_ptr(i + D - (SI - 1));
+        }
+        const uint32_t wj[4] = {wv.x, wv.y, wv.z, wv.w};
+        const uint4* ai = abase + (size_t)ii * 4 * MR * 4;
+        const float* ci = cbase + ii * 32;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t p[4];
+            nib_pairs_perm(wj[j], p);
+            const uint4 bq = make_uint4(p[0], p[1], p[2], p[3]);
+            const uint4 aq = ai[j * MR * 4];
+            const float4 cb = *(const float4*)(ci + j * 8);
+            const float4_t c = {cb.x, cb.y, cb.z, cb.w};
+            const float4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, aq), __builtin_bit_cast(bf16x8_t, bq), c, 0, 0, 0);
+            // software pipeline: scale the previous group while this MFMA runs
+#pragma unroll
+            for (int e = 0; e < ACC; e++) acc[e] = __builtin_fmaf(sprev, dprev[e], acc[e]);
+            dprev = d;
+            sprev = sj[j];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    const int nbatch = (nmine + D - 1) / D;
+    for (int bt = 0; bt + 1 < nbatch; bt++) {
+#pragma unroll
+        for (int u = 0; u < D; u++) step(std::true_type{}, u, bt * D + u);
+    }
+    if (nbatch > 0) {
+#pragma unroll
+        for (int u = 0; u < D; u++) step(std::false_type{}, u, (nbatch - 1) * D + u);
+    }
+#pragma unroll
+    for (int e = 0; e < ACC; e++) acc[e] = __builtin_fmaf(sprev, dprev[e], acc[e]);
+
+    // lane (q, r) holds D rows 4q..4q+3 of column r
+    if (q * 4 < MR) {
+#pragma unroll
+        for (int e = 0; e < ACC; e++)
+            if (4 * q + e < MR) red[(wave * 8 + 4 * q + e) * 16 + r] = acc[e];
     }
     __syncthreads();
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
-        float v = red[(0 * M + m) * 16 + rr] + red[(1 * M + m) * 16 + rr];
-        v += red[(2 * M + m) * 16 + rr];
-        v += red[(3 * M + m) * 16 + rr];
+        float v;
+        if (XF32) {
+            v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) v += red[(w * 8 + 2 * m) * 16 + rr] + red[(w * 8 + 2 * m + 1) * 16 + rr];
+        } else {
+            v = red[(0 * 8 + m) * 16 + rr] + red[(1 * 8 + m) * 16 + rr];
+            v += red[(2 * 8 + m) * 16 + rr];
+            v += red[(3 * 8 + m) * 16 + rr];
+        }
         const int n = t * 16 + rr;
         if (n < N) epi(m, n, v);
     }
@@ -286,17 +433,19 @@ struct Q8GemvSmem {
     static size_t bytes(int Kp) { return (size_t)M * Kp * 4 + (size_t)M * (Kp / 16) * 4 + 4 * 16 * M * 4; }
 };
 
-template <int M, bool XF32, bool PER_ROW, typename Epi>
+template <int M, bool XF32, bool VEC, bool PER_ROW, typename Epi>
 __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ wt,
                                                       const float* __restrict__ sc,
                                                       const void* __restrict__ xin, int K, int Kp,
                                                       int N, int ldx, Epi epi) {
-    constexpr int U = 4;
+    constexpr int D = 8;
+    constexpr int XB = 4;  // 16-element x chunks per thread loaded ahead of the weights
     extern __shared__ uint4 smem[];
     const int NCH = Kp >> 6;  // 64-element chunks
+    const int N16 = Kp >> 4;  // 16-element chunks per x row
     float* xl = (float*)smem;                 // [M][Kp]
     float* bias = xl + (size_t)M * Kp;        // [M][Kp/16]
-    float* red = bias + (size_t)M * (Kp / 16);
+    float* red = bias + (size_t)M * N16;
 
     const int t = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -305,26 +454,60 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
     const uint4* wp = wt + (size_t)t * NCH * 64 + lane;
     const int row = t * 16 + r;
     const int GPR = Kp >> 5;  // groups per row (per-group scales)
+    const int nchunks = M * N16;
+    auto item_off = [&](int i) { return (size_t)(i < nmine ? wave + 4 * i : 0) * 64; };
 
-    uint4 wcur[U];
+    uint4 xa[XB][2], xb[XB][2];
 #pragma unroll
-    for (int u = 0; u < U; u++)
-        if (u < nmine) wcur[u] = ldg_stream(wp + (size_t)(wave + 4 * u) * 64);
+    for (int b = 0; b < XB; b++) {
+        int c = tid + b * 256;
+        c = c < nchunks ? c : nchunks - 1;
+        const int m = c / N16, k0 = (c - m * N16) * 16;
+        load_x8<XF32, VEC>(xin, m, ldx, K, k0, xa[b][0], xb[b][0]);
+        load_x8<XF32, VEC>(xin, m, ldx, K, k0 + 8, xa[b][1], xb[b][1]);
+    }
+    uint4 wbuf[D];
+#pragma unroll
+    for (int u = 0; u < D; u++) wbuf[u] = ldg_stream(wp + item_off(u));
 
-    for (int c = tid; c < M * (Kp / 16); c += 256) {
-        const int m = c / (Kp / 16), cc = c - m * (Kp / 16);
-        const int k0 = cc * 16;
+    auto stage = [&](int c, const uint4 a[2], const uint4 b[2]) {
+        const int m = c / N16, c16 = c - m * N16;
+        float* dst = xl + (size_t)m * Kp + c16 * 16;
         float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            float v;
-            int k = k0 + i;
-            if (XF32) v = (k < K) ? ((const float*)xin)[(size_t)m * ldx + k] : 0.0f;
-            else v = (k < K) ? bf16_bits_to_f32(((const uint16_t*)xin)[(size_t)m * ldx + k]) : 0.0f;
-            xl[(size_t)m * Kp + k] = v;
-            s += v;
+        for (int h = 0; h < 2; h++) {
+            float v[8];
+            if (XF32) {
+                v[0] = __uint_as_float(a[h].x); v[1] = __uint_as_float(a[h].y);
+                v[2] = __uint_as_float(a[h].z); v[3] = __uint_as_float(a[h].w);
+                v[4] = __uint_as_float(b[h].x); v[5] = __uint_as_float(b[h].y);
+                v[6] = __uint_as_float(b[h].z); v[7] = __uint_as_float(b[h].w);
+            } else {
+                const uint32_t w4[4] = {a[h].x, a[h].y, a[h].z, a[h].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v[2 * i] = bf16_bits_to_f32(w4[i] & 0xFFFF);
+                    v[2 * i + 1] = bf16_bits_to_f32(w4[i] >> 16);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) s += v[i];
+            *(float4*)(dst + h * 8) = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4*)(dst + h * 8 + 4) = make_float4(v[4], v[5], v[6], v[7]);
         }
-        bias[(size_t)m * (Kp / 16) + cc] = -128.0f * s;
+        bias[(size_t)m * N16 + c16] = -128.0f * s;
+    };
+#pragma unroll
+    for (int b = 0; b < XB; b++) {
+        const int c = tid + b * 256;
+        if (c < nchunks) stage(c, xa[b], xb[b]);
+    }
+    for (int c = tid + XB * 256; c < nchunks; c += 256) {
+        uint4 a[2], b2[2];
+        const int m = c / N16, k0 = (c - m * N16) * 16;
+        load_x8<XF32, VEC>(xin, m, ldx, K, k0, a[0], b2[0]);
+        load_x8<XF32, VEC>(xin, m, ldx, K, k0 + 8, a[1], b2[1]);
+        stage(c, a, b2);
     }
     __syncthreads();
 
@@ -332,43 +515,39 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
 #pragma unroll
     for (int m = 0; m < M; m++) acc[m] = 0.0f;
 
-    for (int base = 0; base < nmine; base += U) {
-        uint4 wnxt[U];
+    auto step = [&](auto refill_tag, int u, int i) {
+        const bool valid = i < nmine;
+        const int c = valid ? wave + 4 * i : 0;
+        const uint32_t wv[4] = {wbuf[u].x ^ 0x80808080u, wbuf[u].y ^ 0x80808080u,
+                                wbuf[u].z ^ 0x80808080u, wbuf[u].w ^ 0x80808080u};
+        if constexpr (decltype(refill_tag)::value) wbuf[u] = ldg_stream(wp + item_off(i + D));
+        const int k0 = c * 64 + q * 16;
+        float s = valid ? 1.0f : 0.0f;
+        if (!PER_ROW) s = valid ? sc[(size_t)row * GPR + (k0 >> 5)] : 0.0f;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int i = base + U + u;
-            if (i < nmine) wnxt[u] = ldg_stream(wp + (size_t)(wave + 4 * i) * 64);
-        }
+        for (int m = 0; m < M; m++) {
+            const float4* xp = (const float4*)(xl + (size_t)m * Kp + k0);
+            float d = bias[(size_t)m * N16 + (k0 >> 4)];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int i = base + u;
-            if (i < nmine) {
-                const int c = wave + 4 * i;
-                const uint32_t wv[4] = {wcur[u].x ^ 0x80808080u, wcur[u].y ^ 0x80808080u,
-                                        wcur[u].z ^ 0x80808080u, wcur[u].w ^ 0x80808080u};
-                const int k0 = c * 64 + q * 16;
-                float s = 1.0f;
-                if (!PER_ROW) s = sc[(size_t)row * GPR + (k0 >> 5)];
-#pragma unroll
-                for (int m = 0; m < M; m++) {
-                    const float4* xp = (const float4*)(xl + (size_t)m * Kp + k0);
-                    float d = bias[(size_t)m * (Kp / 16) + (k0 >> 4)];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const float4 xv = xp[j];
-                        const uint32_t w = wv[j];
-                        d = __builtin_fmaf((float)(w & 0xFF), xv.x, d);
-                        d = __builtin_fmaf((float)((w >> 8) & 0xFF), xv.y, d);
-                        d = __builtin_fmaf((float)((w >> 16) & 0xFF), xv.z, d);
-                        d = __builtin_fmaf((float)(w >> 24), xv.w, d);
-                    }
-                    if (PER_ROW) acc[m] += d;
-                    else acc[m] = __builtin_fmaf(s, d, acc[m]);
-                }
+            for (int j = 0; j < 4; j++) {
+                const float4 xv = xp[j];
+                const uint32_t w = wv[j];
+                d = __builtin_fmaf((float)(w & 0xFF), xv.x, d);
+                d = __builtin_fmaf((float)((w >> 8) & 0xFF), xv.y, d);
+                d = __builtin_fmaf((float)((w >> 16) & 0xFF), xv.z, d);
+                d = __builtin_fmaf((float)(w >> 24), xv.w, d);
             }
+            acc[m] = __builtin_fmaf(s, d, acc[m]);
         }
+    };
+    const int nbatch = (nmine + D - 1) / D;
+    for (int bt = 0; bt + 1 < nbatch; bt++) {
 #pragma unroll
-        for (int u = 0; u < U; u++) wcur[u] = wnxt[u];
+        for (int u = 0; u < D; u++) step(std::true_type{}, u, bt * D + u);
+    }
+    if (nbatch > 0) {
+#pragma unroll
+        for (int u = 0; u < D; u++) step(std::false_type{}, u, (nbatch - 1) * D + u);
     }
 
 #pragma unroll
@@ -504,7 +683,7 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
         for (int a = 0; a < RT; a++) {
             int tt = min(tile0 + a, NT - 1);
             w[a] = ldg_stream(wt + ((size_t)tt * GQ + gq) * 64 + lane);
-            s.load(sc + ((size_t)tt * GQ + gq) * 64 + r * 4, a);
+            s.load(sc + q4_scale_index(std::is_same<ST, _Float16>::value, tt, gq, r, 0, GQ), a);
         }
     };
     if (gq0 < gq1) {
