@@ -225,12 +225,12 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // ("items"), stages only the activations it needs in its own LDS region
 // (no workgroup barrier) and keeps D group-quads of weights in flight.
 // ---------------------------------------------------------------------------
-template <int MR, bool XF32, bool VEC, typename ST, typename Epi>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MR <= 1 ? 4 : 2))) void q4_gemv_kernel(const uint4* __restrict__ wt,
+template <int MR, bool XF32, bool VEC, typename ST, typename Epi, int D = 2, int WPE = 4>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemv_kernel(const uint4* __restrict__ wt,
                                                       const ST* __restrict__ sc,
                                                       const void* __restrict__ xin, int K, int Kp,
                                                       int N, int ldx, Epi epi) {
-    constexpr int D = 8;          // items in flight per wave (rolling prefetch)
+    // D: items in flight per wave (rolling prefetch); WPE: occupancy target
     constexpr int SI = ScaleRec<ST>::ITEMS;
     constexpr int NS = D / SI;    // scale records in flight
     constexpr int M = XF32 ? MR / 2 : MR;  // activation rows
