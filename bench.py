@@ -1,0 +1,164 @@
+"""Headline benchmark: int4 group-32 GEMV HBM bandwidth (
+11008x4096, M=1, bf16 activations) plus the 7B-shape int4 batch-1 decode rate
+(config 3), on one MI355X.
+
+One "step" is one GEMV launch over one batch (M=1) of synthetic activations.
+The timed loop cycles through enough distinct weight copies (>256 MiB) that
+the weights stream from HBM, not the 256 MB Infinity Cache.  Times come from
+HIP events recorded on the library's own stream (th_bench_linear,
+th_llama_time_steps).  The CPU baseline is the oracle's restatement of the
+reference q4_matvec (crates/tang-infer/src/quantize.rs:256-289), f64,
+single thread, on a bounded sample of the same workload.
+
+Prints ONE JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+from tang_amd import capi  # noqa: E402
+
+METRIC = "Q4 GEMV HBM GB/s (% of peak); decode tok/s, 7B-shape int4, batch 1"
+PEAK_HBM_GBS = 8000.0
+N, K = 11008, 4096
+GEMV_BYTES = {1: 25414656, 4: 25571328, 8: 25780224, 16: 26198016}  # algorithmic bytes per call
+N_COPIES = 12  # 12 x 25.4 MB = 305 MB > 256 MB last-level cache
+
+CFG7B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=32, head_dim=128, d_ff=11008, vocab=32000,
+             max_seq=2176, eps=1e-5, rope_theta=1e4)
+
+
+def gemv_bench(dev, m, steps, warmup):
+    nib, sc16 = capi.synth_q4(2, N, K)
+    ws = [dev.q4_upload_packed(nib, sc16, N, K, capi.F16) for _ in range(N_COPIES)]
+    x = dev.upload(capi.synth_normal(3, m * K, 1.0, capi.BF16), capi.BF16)
+    y = dev.alloc(m * N)
+    if warmup:
+        dev.bench_linear(x, m, ws, y, warmup)
+    ms = dev.bench_linear(x, m, ws, y, steps)
+    for w in ws:
+        w.free()
+    return ms
+
+
+def decode_bytes_per_token(c, t_attended):
+    """Algorithmic HBM bytes of one decode step: every weight byte, the KV
+    rows attended, norms and one embedding row, each counted once."""
+    d, ff, L, V = c["d_model"], c["d_ff"], c["n_layers"], c["vocab"]
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    qd = c["n_heads"] * c["head_dim"]
+    lin = L * (d * (qd + 2 * kvd) + qd * d + 2 * d * ff + ff * d) + V * d
+    weights = lin // 2 + (lin // 32) * 2
+    kv = L * 2 * t_attended * kvd * 2
+    return weights + kv + (2 * L + 1) * d * 2 + d * 2
+
+
+def decode_bench(dev, steps):
+    import ctypes
+    c = CFG7B
+    cfg = capi.LlamaConfig(c["n_layers"], c["d_model"], c["n_heads"], c["n_kv_heads"], c["head_dim"], c["d_ff"],
+                           c["vocab"], c["max_seq"], c["eps"], c["rope_theta"])
+    L = capi.lib()
+    h = ctypes.c_void_p()
+    t0 = time.time()
+    capi.check(L.th_llama_create(dev.handle, ctypes.byref(cfg), ctypes.byref(h)))
+    try:
+        capi.check(L.th_llama_init_synthetic(h, 3))
+        capi.check(L.th_llama_fill_kv_synthetic(h, 2048, 33))
+        init_s = time.time() - t0
+        ms = ctypes.c_float()
+        capi.check(L.th_llama_time_steps(h, 1, 2048, 8, ctypes.byref(ms)))  # warm (graph build)
+        capi.check(L.th_llama_fill_kv_synthetic(h, 2048, 33))
+        capi.check(L.th_llama_time_steps(h, 1, 2048, steps, ctypes.byref(ms)))
+    finally:
+        L.th_llama_destroy(h)
+    per_tok_ms = ms.value / steps
+    mean_bytes = np.mean([decode_bytes_per_token(c, 2049 + i) for i in range(steps)])
+    roof_tok_s = PEAK_HBM_GBS * 1e9 / mean_bytes
+    tok_s = 1e3 / per_tok_ms
+    return dict(tok_s=round(tok_s, 1), ms_per_token=round(per_tok_ms, 4), steps=steps,
+                bytes_per_token_mean=int(mean_bytes), roofline_tok_s=round(roof_tok_s, 1),
+                frac_of_roofline=round(tok_s / roof_tok_s, 4), kv_positions="2049..%d" % (2048 + steps),
+                init_s=round(init_s, 1))
+
+
+def cpu_baseline(budget_s=12.0):
+    """Oracle q4_matvec (f64, one thread) on config-2 rows: a bounded sample."""
+    import oracle
+    nib, sc16 = capi.synth_q4(2, N, K)
+    sc = oracle.f16_to_f32(sc16)
+    x = oracle.bf16_to_f32(capi.synth_normal(3, K, 1.0, capi.BF16)).astype(np.float64)
+    rows = 1376  # 1/8 of the matrix per call
+    calls, t0 = 0, time.time()
+    while time.time() - t0 < budget_s:
+        r0 = (calls * rows) % N
+        oracle.q4_matvec_soa(nib[r0:r0 + rows], sc[r0:r0 + rows], rows, K, x, threads=1)
+        calls += 1
+    dt = time.time() - t0
+    full_calls = calls * rows / N
+    us = dt / full_calls * 1e6
+    return dict(value=round(GEMV_BYTES[1] / us / 1e3, 3), unit="GB/s", cores=1, kind="port",
+                sample="%d calls of q4_matvec on %d of the %d rows (%.1f s, %.0f us per full 11008x4096 call)"
+                       % (calls, rows, N, dt, us))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2400)
+    ap.add_argument("--warmup", type=int, default=240)
+    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (collectives are out of scope); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    dev = capi.HipComputeDevice(0)
+    ms = gemv_bench(dev, 1, args.steps, args.warmup)
+    us = ms * 1e3 / args.steps
+    gbs = GEMV_BYTES[1] / us / 1e3
+    extra = {}
+    for m in (4, 8, 16):
+        msm = gemv_bench(dev, m, max(args.steps // 4, 48), 24)
+        usm = msm * 1e3 / max(args.steps // 4, 48)
+        extra["M=%d" % m] = dict(us=round(usm, 3), gbs=round(GEMV_BYTES[m] / usm / 1e3, 1),
+                                 frac=round(GEMV_BYTES[m] / usm / 1e3 / PEAK_HBM_GBS, 4))
+    decode = None if args.no_decode else decode_bench(dev, args.decode_steps)
+    cpu = None if args.no_cpu else cpu_baseline()
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded xoshiro256**; int4 ~U[-8,7], f16 scales ~U[0.002,0.01], x bf16 ~N(0,1))",
+        "config": {"workload": "q4 g32 GEMV 11008x4096, M=1, bf16 activations (BASELINE config 2), "
+                               "%d rotating weight copies (305 MB > 256 MB MALL)" % N_COPIES,
+                   "M_sweep": extra},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "decode_7b": decode,
+    }
+    print(json.dumps(out))
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

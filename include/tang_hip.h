@@ -194,6 +194,10 @@ int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, in
  * and argmax written to the model's device-side token slot. */
 int th_llama_step_device(th_llama* m, size_t pos);
 int th_llama_set_token(th_llama* m, int32_t token);
+/* Benchmark helper: run n_steps greedy steps from (token, pos) as in
+ * th_llama_generate and return the milliseconds between HIP events recorded
+ * on the device stream around the step launches. */
+int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, float* ms);
 
 /* ---- MoE (DeepSeek-style; no reference implementation) ------------------ */
 typedef struct th_moe th_moe;

@@ -86,6 +86,7 @@ SIGNATURES = {
     "th_llama_generate": ([_P, ctypes.c_int32, _S, _S, _P, _P], _I),
     "th_llama_step_device": ([_P, _S], _I),
     "th_llama_set_token": ([_P, ctypes.c_int32], _I),
+    "th_llama_time_steps": ([_P, ctypes.c_int32, _S, _S, _P], _I),
     "th_moe_create": ([_P, _S, _S, _S, _S, _S, _P], _I),
     "th_moe_destroy": ([_P], _I),
     "th_moe_init_synthetic": ([_P, _U64], _I),

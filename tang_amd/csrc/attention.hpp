@@ -37,11 +37,13 @@ __device__ __forceinline__ void load8<float>(const float* p, float v[8]) {
 // One (head, query, chunk) per workgroup of 256 threads.  LPK = D/8 lanes
 // share one key (eight elements each); the block walks 4*64/LPK keys per step.
 // part[(qi*H + h)*n_splits + s] = {m, l, acc[D]}.
+// cache_start_dev (optional): read cache_start from device memory instead, so
+// one captured launch serves every decode position.
 template <int D, typename CT>
 __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict__ q, const CT* __restrict__ kc,
                                                          const CT* __restrict__ vc, int cache_start, int n_heads,
                                                          int n_kv_heads, int chunk, int n_splits,
-                                                         float* __restrict__ part) {
+                                                         float* __restrict__ part, const int* cache_start_dev = nullptr) {
     constexpr int LPK = D / 8;
     constexpr int KPB = 256 / LPK;  // keys per block step
     __shared__ float sc[256];
@@ -52,6 +54,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
     const int slot = tid / LPK, e = tid % LPK;
     const int kv_dim = n_kv_heads * D;
     const int kv_h = h / (n_heads / n_kv_heads);
+    if (cache_start_dev) cache_start = *cache_start_dev;
     const int attend = cache_start + qi + 1;
     const int j0 = s * chunk;
     const int len = max(0, min(chunk, attend - j0));
@@ -113,8 +116,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
 }
 
 // Merge the chunk records of one (head, query): out = sum acc_s e^{m_s-M} / sum l_s e^{m_s-M}.
+template <bool OUT_BF16 = false>
 __global__ void attn_combine_kernel(const float* __restrict__ part, int n_heads, int D, int n_splits,
-                                    float* __restrict__ out) {
+                                    void* __restrict__ out) {
     const int h = blockIdx.x, qi = blockIdx.y;
     const float* recs = part + (size_t)(qi * n_heads + h) * n_splits * (D + 2);
     float M = -INFINITY;
@@ -131,7 +135,9 @@ __global__ void attn_combine_kernel(const float* __restrict__ part, int n_heads,
             const float m = recs[(size_t)s * (D + 2)];
             if (m != -INFINITY) a += recs[(size_t)s * (D + 2) + 2 + d] * expf(m - M);
         }
-        out[((size_t)qi * n_heads + h) * D + d] = a * inv;
+        const size_t o = ((size_t)qi * n_heads + h) * D + d;
+        if (OUT_BF16) ((uint16_t*)out)[o] = f32_to_bf16_rne(a * inv);
+        else ((float*)out)[o] = a * inv;
     }
 }
 
@@ -147,8 +153,8 @@ inline void launch_attn_split_d(const float* q, const void* kc, const void* vc, 
         hipLaunchKernelGGL((attn_split_kernel<D, float>), grid, dim3(256), 0, s, q, (const float*)kc, (const float*)vc,
                            cache_start, n_heads, n_kv_heads, chunk, n_splits, part);
     TH_LAUNCH_CHECK();
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)n_heads, (unsigned)q_len), dim3(D < 256 ? D : 256), 0, s,
-                       part, n_heads, D, n_splits, out);
+    hipLaunchKernelGGL(attn_combine_kernel<false>, dim3((unsigned)n_heads, (unsigned)q_len), dim3(D < 256 ? D : 256), 0,
+                       s, part, n_heads, D, n_splits, (void*)out);
     TH_LAUNCH_CHECK();
 }
 

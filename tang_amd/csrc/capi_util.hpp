@@ -24,6 +24,11 @@
 
 namespace th {
 
+// Rethrow the failure of a nested C entry point.
+inline void check_status(int rc) {
+    if (rc != TH_OK) throw Error(rc, std::string("nested call failed: ") + th_last_error());
+}
+
 // Grow-only stream-ordered workspace owned by the device.
 void* device_scratch(th_device* dev, size_t bytes);
 void require_len(const th_buffer* b, th_dtype dt, size_t n, const char* what);

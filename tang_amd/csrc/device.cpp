@@ -65,7 +65,9 @@ th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_d
     const size_t ssz = dtype_size(sdt);
     const bool f16 = sdt == TH_F16;
     std::vector<uint8_t> stile(q4_scale_count(f16, NT, GQ) * ssz, 0);
-    for (size_t row = 0; row < rows; row++) {
+#pragma omp parallel for schedule(static)
+    for (long rowl = 0; rowl < (long)rows; rowl++) {
+        const size_t row = (size_t)rowl;
         const size_t t = row / 16, rr = row % 16;
         for (size_t g = 0; g < bpr; g++) {
             const size_t gq = g / 4, j = g % 4;

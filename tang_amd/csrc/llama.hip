@@ -1,0 +1,468 @@
+// Device-resident Llama-style decode engine with int4 group-32 weights.
+//
+// One decode step restates crates/tang-train/examples/smollm.rs:215-300
+// (pre-norm -> attention -> +residual -> pre-norm -> SwiGLU MLP -> +residual,
+// final norm, LM head) with the ComputeDevice ops of the reference
+// (rms_norm cpu.rs:126, rope device.rs:582, kv_attention cpu.rs:257,
+// swiglu device.rs:727) and greedy sampling (sampling.rs:184).  Rounding
+// points: every linear reads its input as bf16 (cuda.rs:22 rounding), K/V are
+// stored f16, the residual stream and all other values are f32.
+//
+// Per layer the step is five kernels plus two norms:
+//   rmsnorm -> QKV GEMV (epilogue: RoPE, f16 K/V append) -> attention chunks
+//   -> combine (bf16) -> O GEMV (epilogue: +residual) -> rmsnorm
+//   -> gate/up GEMV (epilogue: SwiGLU, bf16) -> down GEMV (+residual)
+// and the whole step (every layer, LM head, argmax, position update) is
+// captured once into a HIP graph that reads the position and token from
+// device memory, so each token is one graph launch with no host round trip.
+#include <vector>
+
+#include "attention.hpp"
+#include "capi_util.hpp"
+#include "ops.hpp"
+#include "qlinear.hpp"
+
+namespace th {
+
+// Tensor ids for th_synth_seed(seed, layer, id).
+enum : int { T_WQ = 0, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_ATTN_NORM, T_FFN_NORM,
+             T_EMBED = 10, T_FINAL_NORM, T_LM_HEAD, T_KCACHE = 20, T_VCACHE };
+
+constexpr float Q4_SMIN = 0.002f, Q4_SMAX = 0.01f, NORM_STD = 0.02f;
+constexpr int ATTN_CHUNK = 64;
+
+// state[0] = position, state[1] = current token, state[2] = steps taken
+struct LlamaState { int pos, token, step, pad; };
+
+// ---------------------------------------------------------------------------
+// kernels
+// ---------------------------------------------------------------------------
+
+__global__ void llama_embed_kernel(const uint16_t* __restrict__ embed, const LlamaState* __restrict__ st, int d,
+                                   float* __restrict__ x) {
+    const size_t base = (size_t)st->token * d;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
+        x[i] = __uint_as_float((uint32_t)embed[base + i] << 16);
+}
+
+// rms_norm (cpu.rs:126-149) of the f32 residual with bf16 weights, written
+// as the bf16 input of the next linear.
+__global__ __launch_bounds__(256) void llama_rmsnorm_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                            int d, float eps, uint16_t* __restrict__ out) {
+    __shared__ float red[256];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < d; i += 256) s += x[i] * x[i];
+    s = block_sum_256(s, red);
+    const float inv = 1.0f / sqrtf(s / (float)d + eps);
+    for (int i = threadIdx.x; i < d; i += 256)
+        out[i] = f32_to_bf16_rne(x[i] * inv * __uint_as_float((uint32_t)w[i] << 16));
+}
+
+// QKV epilogue: rows [0,qd) are q, [qd,qd+kvd) k, then v.  q and k get the
+// interleaved RoPE of device.rs:582-610 at the device-side position; k and v
+// are appended to the f16 cache row `pos`.
+struct EpiQKV {
+    float* q; _Float16* kc; _Float16* vc;
+    const float* cs; const float* sn; const LlamaState* st;
+    int qd, kvd, hd;
+    __device__ __forceinline__ void operator()(int, int n, float v, const float* tile) const {
+        const int pos = st->pos;
+        const int rr = n & 15;
+        float out = v;
+        if (n < qd + kvd) {
+            const int half = hd / 2;
+            const int i = (n % hd) >> 1;
+            const float c = cs[(size_t)pos * half + i], s = sn[(size_t)pos * half + i];
+            if ((rr & 1) == 0) {
+                const float x0 = v, x1 = tile[rr + 1];
+                out = x0 * c - x1 * s;
+            } else {
+                const float x0 = tile[rr - 1], x1 = v;
+                out = x0 * s + x1 * c;
+            }
+        }
+        if (n < qd) q[n] = out;
+        else if (n < qd + kvd) kc[(size_t)pos * kvd + (n - qd)] = (_Float16)out;
+        else vc[(size_t)pos * kvd + (n - qd - kvd)] = (_Float16)out;
+    }
+};
+
+// y += linear (residual add, device.rs:721 on the f32 stream)
+struct EpiAddTo {
+    float* x;
+    __device__ __forceinline__ void operator()(int, int n, float v, const float*) const { x[n] = x[n] + v; }
+};
+
+// Gate/up tiles hold gate rows 8b..8b+7 then up rows 8b..8b+7: the first
+// eight lanes emit bf16(swiglu(g, u)) for intermediate index 8b + rr.
+struct EpiSwiGLU {
+    uint16_t* out;
+    __device__ __forceinline__ void operator()(int, int n, float v, const float* tile) const {
+        const int rr = n & 15;
+        if (rr < 8) out[(n >> 4) * 8 + rr] = f32_to_bf16_rne(swiglu_f64(v, tile[rr + 8]));
+    }
+};
+
+// Greedy argmax of the logits, then advance the position.
+__global__ __launch_bounds__(256) void llama_argmax_kernel(const float* __restrict__ logits, int vocab, LlamaState* st,
+                                                           int32_t* __restrict__ history) {
+    __shared__ float rv[256];
+    __shared__ int ri[256];
+    float bv; int bi;
+    argmax_block_256(logits, vocab, rv, ri, bv, bi);
+    if (threadIdx.x == 0) {
+        history[st->step] = bi;
+        st->token = bi;
+        st->step += 1;
+        st->pos += 1;
+    }
+}
+
+template <typename Epi>
+static void gemv_bf16(const th_qweight* w, const uint16_t* x, Epi epi, hipStream_t s) {
+    TH_REQUIRE(w->bits == 4 && w->scale_dtype == TH_F16, "engine weights must be q4 with f16 scales");
+    const size_t smem = Q4GemvSmem<1>::bytes((int)(w->Kp / 128));
+    TH_REQUIRE(smem <= 48 * 1024, "engine GEMV LDS above 48 KiB");
+    hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi>), dim3((unsigned)(w->Np / 16)), dim3(256), smem, s,
+                       (const uint4*)w->data, (const _Float16*)w->scales, (const void*)x, (int)w->cols, (int)w->Kp,
+                       (int)w->rows, (int)w->cols, epi);
+    TH_LAUNCH_CHECK();
+}
+
+}  // namespace th
+
+using namespace th;
+
+struct th_llama {
+    th_device* dev = nullptr;
+    th_llama_config cfg{};
+    int qd = 0, kvd = 0, max_steps = 0, n_splits = 0;
+    std::vector<th_qweight*> wqkv, wo, wgu, wd;
+    th_qweight* lm = nullptr;
+    uint16_t *embed = nullptr, *attn_norm = nullptr, *ffn_norm = nullptr, *final_norm = nullptr;
+    _Float16 *kcache = nullptr, *vcache = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    float *x = nullptr, *q = nullptr, *logits = nullptr, *part = nullptr;
+    uint16_t *h = nullptr, *att = nullptr, *sg = nullptr;
+    LlamaState* st = nullptr;
+    int32_t* history = nullptr;
+    hipGraphExec_t graph = nullptr;
+    bool weights_ready = false;
+};
+
+namespace th {
+
+static void llama_free(th_llama* m) {
+    if (!m) return;
+    (void)hipStreamSynchronize(m->dev->stream);
+    for (auto* v : {&m->wqkv, &m->wo, &m->wgu, &m->wd})
+        for (th_qweight* w : *v) th_qweight_free(w);
+    if (m->lm) th_qweight_free(m->lm);
+    void* ptrs[] = {m->embed, m->attn_norm, m->ffn_norm, m->final_norm, m->kcache, m->vcache, m->rope_cos,
+                    m->rope_sin, m->x, m->q, m->logits, m->part, m->h, m->att, m->sg, m->st, m->history};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    delete m;
+}
+
+template <typename T>
+static T* dalloc(size_t n) {
+    void* p = nullptr;
+    TH_HIP(hipMalloc(&p, n * sizeof(T)));
+    return (T*)p;
+}
+
+// Enqueue one decode step (all layers) on the device stream.
+static void llama_enqueue_step(th_llama* m) {
+    const th_llama_config& c = m->cfg;
+    hipStream_t s = m->dev->stream;
+    const int d = c.d_model, hd = c.head_dim;
+    hipLaunchKernelGGL(llama_embed_kernel, dim3(16), dim3(256), 0, s, m->embed, m->st, d, m->x);
+    TH_LAUNCH_CHECK();
+    const size_t cache_layer = (size_t)c.max_seq * m->kvd;
+    for (int l = 0; l < c.n_layers; l++) {
+        _Float16* kc = m->kcache + l * cache_layer;
+        _Float16* vc = m->vcache + l * cache_layer;
+        hipLaunchKernelGGL(llama_rmsnorm_kernel, dim3(1), dim3(256), 0, s, m->x, m->attn_norm + (size_t)l * d, d, c.eps, m->h);
+        TH_LAUNCH_CHECK();
+        gemv_bf16(m->wqkv[l], m->h, EpiQKV{m->q, kc, vc, m->rope_cos, m->rope_sin, m->st, m->qd, m->kvd, hd}, s);
+        dim3 grid((unsigned)c.n_heads, 1, (unsigned)m->n_splits);
+        switch (hd) {
+            case 64:
+                hipLaunchKernelGGL((attn_split_kernel<64, _Float16>), grid, dim3(256), 0, s, m->q, kc, vc, 0, c.n_heads,
+                                   c.n_kv_heads, ATTN_CHUNK, m->n_splits, m->part, (const int*)&m->st->pos);
+                break;
+            case 128:
+                hipLaunchKernelGGL((attn_split_kernel<128, _Float16>), grid, dim3(256), 0, s, m->q, kc, vc, 0, c.n_heads,
+                                   c.n_kv_heads, ATTN_CHUNK, m->n_splits, m->part, (const int*)&m->st->pos);
+                break;
+            default:
+                hipLaunchKernelGGL((attn_split_kernel<256, _Float16>), grid, dim3(256), 0, s, m->q, kc, vc, 0, c.n_heads,
+                                   c.n_kv_heads, ATTN_CHUNK, m->n_splits, m->part, (const int*)&m->st->pos);
+        }
+        TH_LAUNCH_CHECK();
+        hipLaunchKernelGGL(attn_combine_kernel<true>, dim3((unsigned)c.n_heads, 1), dim3(hd < 256 ? hd : 256), 0, s,
+                           m->part, c.n_heads, hd, m->n_splits, (void*)m->att);
+        TH_LAUNCH_CHECK();
+        gemv_bf16(m->wo[l], m->att, EpiAddTo{m->x}, s);
+        hipLaunchKernelGGL(llama_rmsnorm_kernel, dim3(1), dim3(256), 0, s, m->x, m->ffn_norm + (size_t)l * d, d, c.eps, m->h);
+        TH_LAUNCH_CHECK();
+        gemv_bf16(m->wgu[l], m->h, EpiSwiGLU{m->sg}, s);
+        gemv_bf16(m->wd[l], m->sg, EpiAddTo{m->x}, s);
+    }
+    hipLaunchKernelGGL(llama_rmsnorm_kernel, dim3(1), dim3(256), 0, s, m->x, m->final_norm, d, c.eps, m->h);
+    TH_LAUNCH_CHECK();
+    gemv_bf16(m->lm, m->h, EpiStore{m->logits, c.vocab}, s);
+    hipLaunchKernelGGL(llama_argmax_kernel, dim3(1), dim3(256), 0, s, m->logits, c.vocab, m->st, m->history);
+    TH_LAUNCH_CHECK();
+}
+
+static void llama_build_graph(th_llama* m) {
+    if (m->graph) return;
+    hipStream_t s = m->dev->stream;
+    hipGraph_t g;
+    TH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    try {
+        llama_enqueue_step(m);
+    } catch (...) {
+        hipGraph_t dummy;
+        (void)hipStreamEndCapture(s, &dummy);
+        throw;
+    }
+    TH_HIP(hipStreamEndCapture(s, &g));
+    TH_HIP(hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0));
+    TH_HIP(hipGraphDestroy(g));
+}
+
+// Concatenate rows of q4 matrices generated by th_synth_q4 (nib + f16 scales).
+struct HostQ4 {
+    std::vector<uint8_t> nib;
+    std::vector<uint16_t> sc;
+    size_t rows = 0, cols = 0;
+};
+
+static HostQ4 synth_q4_host(uint64_t seed, size_t rows, size_t cols) {
+    HostQ4 h;
+    h.rows = rows; h.cols = cols;
+    const size_t bpr = ceil_div(cols, 32);
+    h.nib.resize(rows * bpr * 16);
+    h.sc.resize(rows * bpr);
+    if (th_synth_q4(seed, rows, cols, Q4_SMIN, Q4_SMAX, h.nib.data(), h.sc.data()) != TH_OK)
+        throw Error(TH_ERR_INVALID, "th_synth_q4 failed");
+    return h;
+}
+
+}  // namespace th
+
+extern "C" {
+
+int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) {
+    TH_API_BEGIN
+    TH_REQUIRE(dev && cfg && out, "null argument");
+    const th_llama_config& c = *cfg;
+    TH_REQUIRE(c.n_layers > 0 && c.d_model > 0 && c.vocab > 0 && c.max_seq > 0, "bad config");
+    TH_REQUIRE(c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256, "head_dim must be 64, 128 or 256");
+    TH_REQUIRE(c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
+    TH_REQUIRE(c.n_heads * c.head_dim == c.d_model, "n_heads*head_dim must equal d_model");
+    TH_REQUIRE(c.d_ff % 8 == 0 && c.d_model % 8 == 0, "d_model and d_ff must be multiples of 8");
+    th_llama* m = new th_llama();
+    try {
+        m->dev = dev;
+        m->cfg = c;
+        m->qd = c.n_heads * c.head_dim;
+        m->kvd = c.n_kv_heads * c.head_dim;
+        m->max_steps = c.max_seq;
+        m->n_splits = (int)ceil_div((size_t)c.max_seq, ATTN_CHUNK);
+        TH_HIP(hipSetDevice(dev->ordinal));
+        const size_t L = c.n_layers, d = c.d_model;
+        m->embed = dalloc<uint16_t>((size_t)c.vocab * d);
+        m->attn_norm = dalloc<uint16_t>(L * d);
+        m->ffn_norm = dalloc<uint16_t>(L * d);
+        m->final_norm = dalloc<uint16_t>(d);
+        m->kcache = dalloc<_Float16>(L * c.max_seq * m->kvd);
+        m->vcache = dalloc<_Float16>(L * c.max_seq * m->kvd);
+        m->rope_cos = dalloc<float>((size_t)c.max_seq * c.head_dim / 2);
+        m->rope_sin = dalloc<float>((size_t)c.max_seq * c.head_dim / 2);
+        m->x = dalloc<float>(d);
+        m->q = dalloc<float>(m->qd);
+        m->logits = dalloc<float>(c.vocab);
+        m->part = dalloc<float>((size_t)c.n_heads * m->n_splits * (c.head_dim + 2));
+        m->h = dalloc<uint16_t>(d);
+        m->att = dalloc<uint16_t>(m->qd);
+        m->sg = dalloc<uint16_t>(c.d_ff);
+        m->st = dalloc<LlamaState>(1);
+        m->history = dalloc<int32_t>(m->max_steps);
+        std::vector<float> cs((size_t)c.max_seq * c.head_dim / 2), sn(cs.size());
+        rope_tables_host(c.head_dim, c.max_seq, c.rope_theta, cs.data(), sn.data());
+        TH_HIP(hipMemcpy(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+        TH_HIP(hipMemcpy(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    } catch (...) {
+        llama_free(m);
+        throw;
+    }
+    *out = m;
+    TH_API_END
+}
+
+int th_llama_destroy(th_llama* m) {
+    TH_API_BEGIN
+    llama_free(m);
+    TH_API_END
+}
+
+int th_llama_init_synthetic(th_llama* m, uint64_t seed) {
+    TH_API_BEGIN
+    TH_REQUIRE(m, "null model");
+    TH_REQUIRE(!m->weights_ready, "weights already initialised");
+    const th_llama_config& c = m->cfg;
+    const size_t d = c.d_model, ff = c.d_ff, L = c.n_layers;
+    m->wqkv.assign(L, nullptr); m->wo.assign(L, nullptr); m->wgu.assign(L, nullptr); m->wd.assign(L, nullptr);
+    const size_t bpr_d = ceil_div(d, 32), bpr_ff = ceil_div(ff, 32);
+    // Host generation runs in parallel over layers; uploads stay serial.
+    std::vector<HostQ4> qkv(L), wo(L), gu(L), dn(L);
+    std::string err;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long l = 0; l < (long)L; l++) {
+        try {
+            HostQ4 q = synth_q4_host(th_synth_seed(seed, l, T_WQ), m->qd, d);
+            HostQ4 k = synth_q4_host(th_synth_seed(seed, l, T_WK), m->kvd, d);
+            HostQ4 v = synth_q4_host(th_synth_seed(seed, l, T_WV), m->kvd, d);
+            HostQ4& f = qkv[l];
+            f.rows = q.rows + k.rows + v.rows; f.cols = d;
+            f.nib = std::move(q.nib); f.nib.insert(f.nib.end(), k.nib.begin(), k.nib.end());
+            f.nib.insert(f.nib.end(), v.nib.begin(), v.nib.end());
+            f.sc = std::move(q.sc); f.sc.insert(f.sc.end(), k.sc.begin(), k.sc.end());
+            f.sc.insert(f.sc.end(), v.sc.begin(), v.sc.end());
+            wo[l] = synth_q4_host(th_synth_seed(seed, l, T_WO), d, d);
+            HostQ4 g = synth_q4_host(th_synth_seed(seed, l, T_WG), ff, d);
+            HostQ4 u = synth_q4_host(th_synth_seed(seed, l, T_WU), ff, d);
+            HostQ4& gi = gu[l];
+            gi.rows = 2 * ff; gi.cols = d;
+            gi.nib.resize(2 * ff * bpr_d * 16);
+            gi.sc.resize(2 * ff * bpr_d);
+            for (size_t b = 0; b < ff / 8; b++) {
+                for (size_t r = 0; r < 8; r++) {
+                    const size_t src = 8 * b + r, dg = 16 * b + r, du = 16 * b + 8 + r;
+                    std::memcpy(&gi.nib[dg * bpr_d * 16], &g.nib[src * bpr_d * 16], bpr_d * 16);
+                    std::memcpy(&gi.nib[du * bpr_d * 16], &u.nib[src * bpr_d * 16], bpr_d * 16);
+                    std::memcpy(&gi.sc[dg * bpr_d], &g.sc[src * bpr_d], bpr_d * 2);
+                    std::memcpy(&gi.sc[du * bpr_d], &u.sc[src * bpr_d], bpr_d * 2);
+                }
+            }
+            dn[l] = synth_q4_host(th_synth_seed(seed, l, T_WD), d, ff);
+            (void)bpr_ff;
+        } catch (const std::exception& e) {
+#pragma omp critical
+            err = e.what();
+        }
+    }
+    if (!err.empty()) throw Error(TH_ERR_INVALID, err);
+    for (size_t l = 0; l < L; l++) {
+        m->wqkv[l] = q4_pack(m->dev, qkv[l].nib.data(), qkv[l].sc.data(), TH_F16, qkv[l].rows, d);
+        m->wo[l] = q4_pack(m->dev, wo[l].nib.data(), wo[l].sc.data(), TH_F16, d, d);
+        m->wgu[l] = q4_pack(m->dev, gu[l].nib.data(), gu[l].sc.data(), TH_F16, 2 * ff, d);
+        m->wd[l] = q4_pack(m->dev, dn[l].nib.data(), dn[l].sc.data(), TH_F16, d, ff);
+        qkv[l] = HostQ4(); wo[l] = HostQ4(); gu[l] = HostQ4(); dn[l] = HostQ4();
+    }
+    {
+        HostQ4 lm = synth_q4_host(th_synth_seed(seed, L, T_LM_HEAD), c.vocab, d);
+        m->lm = q4_pack(m->dev, lm.nib.data(), lm.sc.data(), TH_F16, c.vocab, d);
+    }
+    std::vector<uint16_t> buf((size_t)c.vocab * d);
+    check_status(th_synth_normal(th_synth_seed(seed, L, T_EMBED), buf.size(), NORM_STD, TH_BF16, buf.data()));
+    TH_HIP(hipMemcpy(m->embed, buf.data(), buf.size() * 2, hipMemcpyHostToDevice));
+    for (size_t l = 0; l < L; l++) {
+        check_status(th_synth_normal(th_synth_seed(seed, l, T_ATTN_NORM), d, NORM_STD, TH_BF16, buf.data()));
+        TH_HIP(hipMemcpy(m->attn_norm + l * d, buf.data(), d * 2, hipMemcpyHostToDevice));
+        check_status(th_synth_normal(th_synth_seed(seed, l, T_FFN_NORM), d, NORM_STD, TH_BF16, buf.data()));
+        TH_HIP(hipMemcpy(m->ffn_norm + l * d, buf.data(), d * 2, hipMemcpyHostToDevice));
+    }
+    check_status(th_synth_normal(th_synth_seed(seed, L, T_FINAL_NORM), d, NORM_STD, TH_BF16, buf.data()));
+    TH_HIP(hipMemcpy(m->final_norm, buf.data(), d * 2, hipMemcpyHostToDevice));
+    m->weights_ready = true;
+    TH_API_END
+}
+
+int th_llama_fill_kv_synthetic(th_llama* m, size_t len, uint64_t seed) {
+    TH_API_BEGIN
+    TH_REQUIRE(m, "null model");
+    TH_REQUIRE(len <= (size_t)m->cfg.max_seq, "len beyond max_seq");
+    const size_t L = m->cfg.n_layers, n = len * m->kvd, layer = (size_t)m->cfg.max_seq * m->kvd;
+    std::vector<std::vector<uint16_t>> k(L), v(L);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long l = 0; l < (long)L; l++) {
+        k[l].resize(n); v[l].resize(n);
+        th_synth_normal(th_synth_seed(seed, l, T_KCACHE), n, 1.0f, TH_F16, k[l].data());
+        th_synth_normal(th_synth_seed(seed, l, T_VCACHE), n, 1.0f, TH_F16, v[l].data());
+    }
+    for (size_t l = 0; l < L; l++) {
+        TH_HIP(hipMemcpy(m->kcache + l * layer, k[l].data(), n * 2, hipMemcpyHostToDevice));
+        TH_HIP(hipMemcpy(m->vcache + l * layer, v[l].data(), n * 2, hipMemcpyHostToDevice));
+    }
+    TH_API_END
+}
+
+int th_llama_set_token(th_llama* m, int32_t token) {
+    TH_API_BEGIN
+    TH_REQUIRE(m, "null model");
+    TH_REQUIRE(token >= 0 && token < m->cfg.vocab, "token out of range");
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    LlamaState s{};
+    TH_HIP(hipMemcpy(&s, m->st, sizeof s, hipMemcpyDeviceToHost));
+    s.token = token;
+    TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    TH_API_END
+}
+
+int th_llama_step_device(th_llama* m, size_t pos) {
+    TH_API_BEGIN
+    TH_REQUIRE(m && m->weights_ready, "model not initialised");
+    TH_REQUIRE(pos < (size_t)m->cfg.max_seq, "position beyond max_seq");
+    LlamaState s{};
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    TH_HIP(hipMemcpy(&s, m->st, sizeof s, hipMemcpyDeviceToHost));
+    s.pos = (int)pos;
+    s.step = 0;
+    TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    llama_build_graph(m);
+    TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+    TH_API_END
+}
+
+int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, int32_t* tokens_out, float* last_logits) {
+    TH_API_BEGIN
+    TH_REQUIRE(m && m->weights_ready, "model not initialised");
+    TH_REQUIRE(token >= 0 && token < m->cfg.vocab, "token out of range");
+    TH_REQUIRE(pos + n_steps <= (size_t)m->cfg.max_seq, "generation runs past max_seq");
+    TH_REQUIRE(n_steps <= (size_t)m->max_steps, "too many steps");
+    if (n_steps == 0) return TH_OK;
+    LlamaState s{(int)pos, token, 0, 0};
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    llama_build_graph(m);
+    for (size_t i = 0; i < n_steps; i++) TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    if (tokens_out) TH_HIP(hipMemcpy(tokens_out, m->history, n_steps * 4, hipMemcpyDeviceToHost));
+    if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
+    TH_API_END
+}
+
+int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, float* ms) {
+    TH_API_BEGIN
+    TH_REQUIRE(m && m->weights_ready && ms, "model not initialised");
+    TH_REQUIRE(token >= 0 && token < m->cfg.vocab, "token out of range");
+    TH_REQUIRE(pos + n_steps <= (size_t)m->cfg.max_seq, "generation runs past max_seq");
+    LlamaState s{(int)pos, token, 0, 0};
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    llama_build_graph(m);
+    TH_HIP(hipEventRecord(m->dev->ev_start, m->dev->stream));
+    for (size_t i = 0; i < n_steps; i++) TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+    TH_HIP(hipEventRecord(m->dev->ev_stop, m->dev->stream));
+    TH_HIP(hipEventSynchronize(m->dev->ev_stop));
+    TH_HIP(hipEventElapsedTime(ms, m->dev->ev_start, m->dev->ev_stop));
+    TH_API_END
+}
+
+}  // extern "C"

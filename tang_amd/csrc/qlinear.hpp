@@ -87,9 +87,14 @@ __device__ __forceinline__ float wave_sum_xor16_32(float v) {
 // Epilogues: receive (batch row m, output column n, f32 value).
 // ---------------------------------------------------------------------------
 
+// `tile` points at the 16 finished values of the current 16-row tile for
+// batch row m (tile[n % 16] == v), so an epilogue can combine neighbouring
+// output rows (RoPE pairs, gate/up halves).
 struct EpiStore {
     float* y; int ldy;
-    __device__ __forceinline__ void operator()(int m, int n, float v) const { y[(size_t)m * ldy + n] = v; }
+    __device__ __forceinline__ void operator()(int m, int n, float v, const float* tile) const {
+        y[(size_t)m * ldy + n] = v;
+    }
 };
 
 // ---------------------------------------------------------------------------
@@ -187,7 +192,7 @@ struct Q4GemvSmem {
     __host__ __device__ static size_t per_wave(int items) { return (size_t)items * 4 * (MR * 64 + 32) + 16; }
     static size_t bytes(int GQ) {
         const int items = (GQ + 3) / 4;
-        return 4 * per_wave(items) + 4 * 8 * 16 * 4;
+        return 4 * per_wave(items) + 4 * 8 * 16 * 4 + 16 * 4 * 4;
     }
 };
 
@@ -404,11 +409,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
             if (4 * q + e < MR) red[(wave * 8 + 4 * q + e) * 16 + r] = acc[e];
     }
     __syncthreads();
+    float* tilev = red + 4 * 8 * 16;  // [M][16]
+    float v = 0.0f;
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
-        float v;
         if (XF32) {
-            v = 0.0f;
 #pragma unroll
             for (int w = 0; w < 4; w++) v += red[(w * 8 + 2 * m) * 16 + rr] + red[(w * 8 + 2 * m + 1) * 16 + rr];
         } else {
@@ -416,8 +421,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
             v += red[(2 * 8 + m) * 16 + rr];
             v += red[(3 * 8 + m) * 16 + rr];
         }
+        tilev[m * 16 + rr] = v;
+    }
+    __syncthreads();
+    if (tid < 16 * M) {
+        const int m = tid >> 4, rr = tid & 15;
         const int n = t * 16 + rr;
-        if (n < N) epi(m, n, v);
+        if (n < N) epi(m, n, v, tilev + m * 16);
     }
 }
 
@@ -430,7 +440,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
 
 template <int M>
 struct Q8GemvSmem {
-    static size_t bytes(int Kp) { return (size_t)M * Kp * 4 + (size_t)M * (Kp / 16) * 4 + 4 * 16 * M * 4; }
+    static size_t bytes(int Kp) { return (size_t)M * Kp * 4 + (size_t)M * (Kp / 16) * 4 + 5 * 16 * M * 4; }
 };
 
 template <int M, bool XF32, bool VEC, bool PER_ROW, typename Epi>
@@ -556,16 +566,22 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
         if (q == 0) red[(wave * M + m) * 16 + r] = v;
     }
     __syncthreads();
+    float* tilev = red + 4 * 16 * M;  // [M][16]
+    float v = 0.0f;
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
-        float v = red[(0 * M + m) * 16 + rr] + red[(1 * M + m) * 16 + rr];
+        v = red[(0 * M + m) * 16 + rr] + red[(1 * M + m) * 16 + rr];
         v += red[(2 * M + m) * 16 + rr];
         v += red[(3 * M + m) * 16 + rr];
         const int n = t * 16 + rr;
-        if (n < N) {
-            if (PER_ROW) v *= sc[n];
-            epi(m, n, v);
-        }
+        if (PER_ROW) v *= sc[n < N ? n : 0];
+        tilev[m * 16 + rr] = v;
+    }
+    __syncthreads();
+    if (tid < 16 * M) {
+        const int m = tid >> 4, rr = tid & 15;
+        const int n = t * 16 + rr;
+        if (n < N) epi(m, n, v, tilev + m * 16);
     }
 }
 

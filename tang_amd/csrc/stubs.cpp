@@ -10,11 +10,4 @@ int th_moe_init_synthetic(th_moe*, uint64_t) { TH_API_BEGIN TH_UNSUPPORTED("th_m
 int th_moe_forward(th_moe*, const th_buffer*, size_t, th_buffer*, th_buffer*, th_buffer*) { TH_API_BEGIN TH_UNSUPPORTED("th_moe_forward"); TH_API_END }
 int th_mla_decode(th_device*, const th_buffer*, const th_buffer*, const th_buffer*, size_t, size_t, size_t, size_t, size_t,
                   size_t, size_t, const th_qweight*, const th_qweight*, float, th_buffer*) { TH_API_BEGIN TH_UNSUPPORTED("th_mla_decode"); TH_API_END }
-int th_llama_create(th_device*, const th_llama_config*, th_llama**) { TH_API_BEGIN TH_UNSUPPORTED("th_llama_create"); TH_API_END }
-int th_llama_destroy(th_llama*) { TH_API_BEGIN TH_UNSUPPORTED("th_llama_destroy"); TH_API_END }
-int th_llama_init_synthetic(th_llama*, uint64_t) { TH_API_BEGIN TH_UNSUPPORTED("th_llama_init_synthetic"); TH_API_END }
-int th_llama_fill_kv_synthetic(th_llama*, size_t, uint64_t) { TH_API_BEGIN TH_UNSUPPORTED("th_llama_fill_kv_synthetic"); TH_API_END }
-int th_llama_generate(th_llama*, int32_t, size_t, size_t, int32_t*, float*) { TH_API_BEGIN TH_UNSUPPORTED("th_llama_generate"); TH_API_END }
-int th_llama_step_device(th_llama*, size_t) { TH_API_BEGIN TH_UNSUPPORTED("th_llama_step_device"); TH_API_END }
-int th_llama_set_token(th_llama*, int32_t) { TH_API_BEGIN TH_UNSUPPORTED("th_llama_set_token"); TH_API_END }
 }
