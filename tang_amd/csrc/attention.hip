@@ -5,9 +5,10 @@
 //
 // Split-K ("flash-decoding") form: each workgroup scores one chunk of
 // positions for one (query, head), keeps the chunk's max m, sum l and
-// unnormalised weighted V, and a combine kernel merges the chunks with
-// exp(m_s - M) weights.  There is no length cap (the reference CUDA kernel
-// holds scores in a fixed 2048-float array, attention_cuda.rs:85).
+// unnormalised weighted V, and the last chunk of each (query, head) to finish
+// merges the chunks with exp(m_s - M) weights (one launch in all).  There is
+// no length cap (the reference CUDA kernel holds scores in a fixed 2048-float
+// array, attention_cuda.rs:85).
 #include "attention.hpp"
 #include "capi_util.hpp"
 #include "ops.hpp"
@@ -64,11 +65,14 @@ void launch_kv_attention(const float* q, const void* kc, const void* vc, bool f1
         return;
     }
     const size_t max_len = cache_start + q_len;
-    const int chunk = attn_chunk_for(max_len, n_heads * q_len, dev ? dev->num_cus : 256);
-    const int n_splits = (int)ceil_div(max_len, (size_t)chunk);
+    // enough 64-position chunks per split that the merge fits in LDS
+    const size_t max_splits = 64 * 1024 / ((head_dim + 2) * sizeof(float));
+    const int subs = (int)std::max<size_t>(1, ceil_div(ceil_div(max_len, (size_t)ATTN_SUB), max_splits));
+    const int n_splits = (int)ceil_div(max_len, (size_t)subs * ATTN_SUB);
     float* part = (float*)device_scratch(dev, q_len * n_heads * n_splits * (head_dim + 2) * sizeof(float));
-    launch_attn_split(q, kc, vc, f16, (int)cache_start, (int)q_len, (int)n_heads, (int)n_kv_heads, (int)head_dim,
-                      chunk, n_splits, part, out, s);
+    int* counters = device_counters(dev, q_len * n_heads);
+    launch_attn_split<false>(q, kc, vc, f16, (int)cache_start, (int)q_len, (int)n_heads, (int)n_kv_heads,
+                             (int)head_dim, subs, n_splits, part, counters, (void*)out, nullptr, s);
 }
 
 }  // namespace th

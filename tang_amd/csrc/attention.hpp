@@ -7,13 +7,6 @@
 
 namespace th {
 
-// Chunk of cache positions per workgroup: small enough that the grid covers
-// the chip about twice.
-inline int attn_chunk_for(size_t max_len, size_t n_rows, int num_cus) {
-    int chunk = 256;
-    while (chunk > 32 && n_rows * ((max_len + chunk - 1) / chunk) < (size_t)num_cus * 2) chunk >>= 1;
-    return chunk;
-}
 
 template <typename CT>
 __device__ __forceinline__ void load8(const CT* p, float v[8]);
@@ -34,21 +27,33 @@ __device__ __forceinline__ void load8<float>(const float* p, float v[8]) {
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-// One (head, query, chunk) per workgroup of 256 threads.  LPK = D/8 lanes
-// share one key (eight elements each); the block walks 4*64/LPK keys per step.
-// part[(qi*H + h)*n_splits + s] = {m, l, acc[D]}.
-// cache_start_dev (optional): read cache_start from device memory instead, so
-// one captured launch serves every decode position.
-template <int D, typename CT>
+// One (head, query, split) per workgroup of 256 threads; a split covers
+// `subs` consecutive chunks of ATTN_SUB = 64 positions.  LPK = D/8 lanes share
+// one key (eight elements each), so the block holds KPB = 256/LPK keys per
+// pass and each thread KPT = 64/KPB keys of a chunk, whose K and V rows are
+// all loaded before any arithmetic.  Chunks merge with the running max
+// (online softmax).  Each split writes {m, l, acc[D]} to
+// part[(qi*H + h)*n_splits + s]; the last split of a (query, head) to finish
+// (counted on counters[qi*H + h], reset on exit) merges all splits in order:
+//   out = sum_s acc_s e^{m_s-M} / sum_s l_s e^{m_s-M},  M = max_s m_s.
+// cache_start_dev (optional): read cache_start from device memory, so one
+// captured launch serves every decode position.
+constexpr int ATTN_SUB = 64;
+
+template <int D, typename CT, bool OUT_BF16>
 __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict__ q, const CT* __restrict__ kc,
                                                          const CT* __restrict__ vc, int cache_start, int n_heads,
-                                                         int n_kv_heads, int chunk, int n_splits,
-                                                         float* __restrict__ part, const int* cache_start_dev = nullptr) {
+                                                         int n_kv_heads, int subs, int n_splits,
+                                                         float* __restrict__ part, int* __restrict__ counters,
+                                                         void* __restrict__ out, const int* cache_start_dev) {
     constexpr int LPK = D / 8;
-    constexpr int KPB = 256 / LPK;  // keys per block step
-    __shared__ float sc[256];
+    constexpr int KPB = 256 / LPK;         // keys per block pass
+    constexpr int KPT = ATTN_SUB / KPB;    // keys per thread per chunk
+    static_assert(KPT >= 1 && KPT * KPB == ATTN_SUB, "chunk must be a multiple of the block pass");
+    __shared__ float sc[ATTN_SUB];
     __shared__ float red[256];
     __shared__ float vacc[KPB][D + 1];
+    __shared__ int s_last;
     const int h = blockIdx.x, qi = blockIdx.y, s = blockIdx.z;
     const int tid = threadIdx.x;
     const int slot = tid / LPK, e = tid % LPK;
@@ -56,116 +61,148 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
     const int kv_h = h / (n_heads / n_kv_heads);
     if (cache_start_dev) cache_start = *cache_start_dev;
     const int attend = cache_start + qi + 1;
-    const int j0 = s * chunk;
-    const int len = max(0, min(chunk, attend - j0));
-    float* rec = part + ((size_t)(qi * n_heads + h) * n_splits + s) * (D + 2);
+    const int split_len = subs * ATTN_SUB;
+    const int j0 = s * split_len;
+    const int len = max(0, min(split_len, attend - j0));
+    float* recs = part + (size_t)(qi * n_heads + h) * n_splits * (D + 2);
+    float* rec = recs + (size_t)s * (D + 2);
     if (len == 0) {
-        for (int i = tid; i < D + 2; i += 256) rec[i] = i == 0 ? -INFINITY : 0.0f;
-        return;
-    }
-    const float scale = 1.0f / sqrtf((float)D);
-    float qv[8];
-    {
-        const float* qp = q + ((size_t)qi * n_heads + h) * D + e * 8;
+        for (int i = tid; i < D + 2; i += 256) st_coherent(&rec[i], i == 0 ? -INFINITY : 0.0f);
+    } else {
+        const float scale = 1.0f / sqrtf((float)D);
+        float qv[8];
+        {
+            const float* qp = q + ((size_t)qi * n_heads + h) * D + e * 8;
 #pragma unroll
-        for (int i = 0; i < 8; i++) qv[i] = qp[i];
-    }
-    const CT* kbase = kc + (size_t)j0 * kv_dim + kv_h * D + e * 8;
-    const CT* vbase = vc + (size_t)j0 * kv_dim + kv_h * D + e * 8;
-    // scores
-    for (int jj = slot; jj < len; jj += KPB) {
-        float kv[8];
-        load8<CT>(kbase + (size_t)jj * kv_dim, kv);
-        float d = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) d += qv[i] * kv[i];
-#pragma unroll
-        for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-        if (e == 0) sc[jj] = d * scale;
-    }
-    __syncthreads();
-    float mx = -INFINITY;
-    for (int i = tid; i < len; i += 256) mx = fmaxf(mx, sc[i]);
-    mx = block_max_256(mx, red);
-    float l = 0.0f;
-    for (int i = tid; i < len; i += 256) {
-        const float p = expf(sc[i] - mx);
-        sc[i] = p;
-        l += p;
-    }
-    l = block_sum_256(l, red);  // includes the barrier that publishes sc
-    float acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    for (int jj = slot; jj < len; jj += KPB) {
-        float vv[8];
-        load8<CT>(vbase + (size_t)jj * kv_dim, vv);
-        const float p = sc[jj];
-#pragma unroll
-        for (int i = 0; i < 8; i++) acc[i] = __builtin_fmaf(p, vv[i], acc[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) vacc[slot][e * 8 + i] = acc[i];
-    __syncthreads();
-    for (int d = tid; d < D; d += 256) {
-        float v = 0.0f;
-        for (int k = 0; k < KPB; k++) v += vacc[k][d];
-        rec[2 + d] = v;
-    }
-    if (tid == 0) { rec[0] = mx; rec[1] = l; }
-}
-
-// Merge the chunk records of one (head, query): out = sum acc_s e^{m_s-M} / sum l_s e^{m_s-M}.
-template <bool OUT_BF16 = false>
-__global__ void attn_combine_kernel(const float* __restrict__ part, int n_heads, int D, int n_splits,
-                                    void* __restrict__ out) {
-    const int h = blockIdx.x, qi = blockIdx.y;
-    const float* recs = part + (size_t)(qi * n_heads + h) * n_splits * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_splits; s++) M = fmaxf(M, recs[(size_t)s * (D + 2)]);
-    float L = 0.0f;
-    for (int s = 0; s < n_splits; s++) {
-        const float m = recs[(size_t)s * (D + 2)];
-        if (m != -INFINITY) L += recs[(size_t)s * (D + 2) + 1] * expf(m - M);
-    }
-    const float inv = 1.0f / L;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float a = 0.0f;
-        for (int s = 0; s < n_splits; s++) {
-            const float m = recs[(size_t)s * (D + 2)];
-            if (m != -INFINITY) a += recs[(size_t)s * (D + 2) + 2 + d] * expf(m - M);
+            for (int i = 0; i < 8; i++) qv[i] = qp[i];
         }
+        float m_run = -INFINITY, l_run = 0.0f;
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+        const int nsub = (len + ATTN_SUB - 1) / ATTN_SUB;
+        for (int c = 0; c < nsub; c++) {
+            const int cj = j0 + c * ATTN_SUB;               // first position of the chunk
+            const int clen = min(ATTN_SUB, len - c * ATTN_SUB);
+            float kv[KPT][8], vv[KPT][8];
+#pragma unroll
+            for (int k = 0; k < KPT; k++) {
+                const int jj = slot + k * KPB;
+                const int row = cj + (jj < clen ? jj : 0);   // clamped: masked below
+                load8<CT>(kc + (size_t)row * kv_dim + kv_h * D + e * 8, kv[k]);
+                load8<CT>(vc + (size_t)row * kv_dim + kv_h * D + e * 8, vv[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < KPT; k++) {
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) d += qv[i] * kv[k][i];
+#pragma unroll
+                for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+                const int jj = slot + k * KPB;
+                if (e == 0) sc[jj] = jj < clen ? d * scale : -INFINITY;
+            }
+            __syncthreads();
+            float mx = -INFINITY;
+            if (tid < ATTN_SUB) mx = sc[tid];
+            mx = block_max_256(mx, red);
+            const float m_new = fmaxf(m_run, mx);
+            const float rescale = expf(m_run - m_new);  // 0 on the first chunk
+            float lsum = 0.0f;
+            if (tid < ATTN_SUB) lsum = tid < clen ? expf(sc[tid] - m_new) : 0.0f;
+            lsum = block_sum_256(lsum, red);
+            l_run = l_run * rescale + lsum;
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i] *= rescale;
+#pragma unroll
+            for (int k = 0; k < KPT; k++) {
+                const int jj = slot + k * KPB;
+                const float p = jj < clen ? expf(sc[jj] - m_new) : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[i] = __builtin_fmaf(p, vv[k][i], acc[i]);
+            }
+            m_run = m_new;
+            __syncthreads();  // sc is rewritten by the next chunk
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) vacc[slot][e * 8 + i] = acc[i];
+        __syncthreads();
+        for (int d = tid; d < D; d += 256) {
+            float v = 0.0f;
+            for (int k = 0; k < KPB; k++) v += vacc[k][d];
+            st_coherent(&rec[2 + d], v);
+        }
+        if (tid == 0) { st_coherent(&rec[0], m_run); st_coherent(&rec[1], l_run); }
+    }
+    // publish this split; the last one to arrive merges
+    if (!last_arrival(&counters[qi * n_heads + h], n_splits, &s_last)) return;
+    // stage every split record into LDS: independent loads, one latency round
+    extern __shared__ float recl[];  // [n_splits][D + 2]
+    const int total = n_splits * (D + 2);
+#pragma unroll 16
+    for (int i = tid; i < total; i += 256) recl[i] = ld_coherent(&recs[i]);
+    __syncthreads();
+    float mloc = -INFINITY;
+    for (int i = tid; i < n_splits; i += 256) mloc = fmaxf(mloc, recl[(size_t)i * (D + 2)]);
+    const float M = block_max_256(mloc, red);
+    float lloc = 0.0f;
+    __shared__ float wts[256];
+    for (int i = tid; i < n_splits; i += 256) {
+        const float m = recl[(size_t)i * (D + 2)];
+        const float w = m == -INFINITY ? 0.0f : expf(m - M);
+        wts[i] = w;
+        lloc += w * recl[(size_t)i * (D + 2) + 1];
+    }
+    const float L = block_sum_256(lloc, red);  // its barriers also publish wts
+    const float inv = 1.0f / L;
+    for (int d = tid; d < D; d += 256) {
+        float a = 0.0f;
+        for (int i = 0; i < n_splits; i++) a += recl[(size_t)i * (D + 2) + 2 + d] * wts[i];
         const size_t o = ((size_t)qi * n_heads + h) * D + d;
         if (OUT_BF16) ((uint16_t*)out)[o] = f32_to_bf16_rne(a * inv);
         else ((float*)out)[o] = a * inv;
     }
 }
 
-template <int D>
+// Dynamic LDS of the split kernel: the merging split stages all records.
+inline size_t attn_merge_lds(int n_splits, int head_dim) { return (size_t)n_splits * (head_dim + 2) * sizeof(float); }
+
+// counters: q_len*n_heads ints, zero on entry and on return.
+template <int D, bool OUT_BF16>
 inline void launch_attn_split_d(const float* q, const void* kc, const void* vc, bool f16, int cache_start, int q_len,
-                                int n_heads, int n_kv_heads, int chunk, int n_splits, float* part, float* out,
-                                hipStream_t s) {
+                                int n_heads, int n_kv_heads, int subs, int n_splits, float* part, int* counters,
+                                void* out, const int* cache_start_dev, hipStream_t s) {
     dim3 grid((unsigned)n_heads, (unsigned)q_len, (unsigned)n_splits);
+    const size_t lds = attn_merge_lds(n_splits, D);
+    TH_REQUIRE(lds <= 64 * 1024, "too many attention splits for the LDS merge");
+    if (lds > 48 * 1024) {
+        TH_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<D, _Float16, OUT_BF16>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        TH_HIP(hipFuncSetAttribute((const void*)attn_split_kernel<D, float, OUT_BF16>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    }
     if (f16)
-        hipLaunchKernelGGL((attn_split_kernel<D, _Float16>), grid, dim3(256), 0, s, q, (const _Float16*)kc,
-                           (const _Float16*)vc, cache_start, n_heads, n_kv_heads, chunk, n_splits, part);
+        hipLaunchKernelGGL((attn_split_kernel<D, _Float16, OUT_BF16>), grid, dim3(256), lds, s, q, (const _Float16*)kc,
+                           (const _Float16*)vc, cache_start, n_heads, n_kv_heads, subs, n_splits, part, counters, out,
+                           cache_start_dev);
     else
-        hipLaunchKernelGGL((attn_split_kernel<D, float>), grid, dim3(256), 0, s, q, (const float*)kc, (const float*)vc,
-                           cache_start, n_heads, n_kv_heads, chunk, n_splits, part);
-    TH_LAUNCH_CHECK();
-    hipLaunchKernelGGL(attn_combine_kernel<false>, dim3((unsigned)n_heads, (unsigned)q_len), dim3(D < 256 ? D : 256), 0,
-                       s, part, n_heads, D, n_splits, (void*)out);
+        hipLaunchKernelGGL((attn_split_kernel<D, float, OUT_BF16>), grid, dim3(256), lds, s, q, (const float*)kc,
+                           (const float*)vc, cache_start, n_heads, n_kv_heads, subs, n_splits, part, counters, out,
+                           cache_start_dev);
     TH_LAUNCH_CHECK();
 }
 
+// subs: 64-position chunks per split; n_splits*(head_dim+2) floats must fit
+// the merge's LDS (64 KiB).
+template <bool OUT_BF16>
 inline void launch_attn_split(const float* q, const void* kc, const void* vc, bool f16, int cache_start, int q_len,
-                              int n_heads, int n_kv_heads, int head_dim, int chunk, int n_splits, float* part,
-                              float* out, hipStream_t s) {
-    TH_REQUIRE(chunk <= 256, "attention chunk above 256");
+                              int n_heads, int n_kv_heads, int head_dim, int subs, int n_splits, float* part,
+                              int* counters, void* out, const int* cache_start_dev, hipStream_t s) {
+    TH_REQUIRE(subs >= 1 && n_splits >= 1 && n_splits <= 256, "attention split count out of range");
     switch (head_dim) {
-        case 64: launch_attn_split_d<64>(q, kc, vc, f16, cache_start, q_len, n_heads, n_kv_heads, chunk, n_splits, part, out, s); break;
-        case 128: launch_attn_split_d<128>(q, kc, vc, f16, cache_start, q_len, n_heads, n_kv_heads, chunk, n_splits, part, out, s); break;
-        case 256: launch_attn_split_d<256>(q, kc, vc, f16, cache_start, q_len, n_heads, n_kv_heads, chunk, n_splits, part, out, s); break;
+        case 64: launch_attn_split_d<64, OUT_BF16>(q, kc, vc, f16, cache_start, q_len, n_heads, n_kv_heads, subs, n_splits, part, counters, out, cache_start_dev, s); break;
+        case 128: launch_attn_split_d<128, OUT_BF16>(q, kc, vc, f16, cache_start, q_len, n_heads, n_kv_heads, subs, n_splits, part, counters, out, cache_start_dev, s); break;
+        case 256: launch_attn_split_d<256, OUT_BF16>(q, kc, vc, f16, cache_start, q_len, n_heads, n_kv_heads, subs, n_splits, part, counters, out, cache_start_dev, s); break;
         default: throw Error(TH_ERR_INVALID, "launch_attn_split: unsupported head_dim");
     }
 }

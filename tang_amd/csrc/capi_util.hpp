@@ -31,6 +31,9 @@ inline void check_status(int rc) {
 
 // Grow-only stream-ordered workspace owned by the device.
 void* device_scratch(th_device* dev, size_t bytes);
+// Zero-initialised ints that kernels leave zero again on exit (arrival
+// counters of the last-workgroup merges); grow-only.
+int* device_counters(th_device* dev, size_t n);
 void require_len(const th_buffer* b, th_dtype dt, size_t n, const char* what);
 void require_len_any(const th_buffer* b, size_t n, const char* what);
 

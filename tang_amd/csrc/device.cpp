@@ -30,6 +30,21 @@ void* device_scratch(th_device* dev, size_t bytes) {
     return dev->scratch;
 }
 
+int* device_counters(th_device* dev, size_t n) {
+    if (n <= dev->n_counters) return dev->counters;
+    if (dev->counters) {
+        TH_HIP(hipStreamSynchronize(dev->stream));
+        TH_HIP(hipFree(dev->counters));
+        dev->counters = nullptr;
+        dev->n_counters = 0;
+    }
+    const size_t want = std::max(n, (size_t)4096);
+    TH_HIP(hipMalloc(&dev->counters, want * sizeof(int)));
+    TH_HIP(hipMemset(dev->counters, 0, want * sizeof(int)));
+    dev->n_counters = want;
+    return dev->counters;
+}
+
 static void check_buf(const th_buffer* b, const char* what) {
     if (!b || !b->ptr && b->n) throw Error(TH_ERR_INVALID, std::string("null buffer: ") + what);
 }
@@ -206,6 +221,7 @@ int th_device_destroy(th_device* d) {
     (void)hipSetDevice(d->ordinal);
     (void)hipStreamSynchronize(d->stream);
     if (d->scratch) (void)hipFree(d->scratch);
+    if (d->counters) (void)hipFree(d->counters);
     (void)hipEventDestroy(d->ev_start);
     (void)hipEventDestroy(d->ev_stop);
     (void)hipStreamDestroy(d->stream);

@@ -8,13 +8,16 @@
 // points: every linear reads its input as bf16 (cuda.rs:22 rounding), K/V are
 // stored f16, the residual stream and all other values are f32.
 //
-// Per layer the step is five kernels plus two norms:
-//   rmsnorm -> QKV GEMV (epilogue: RoPE, f16 K/V append) -> attention chunks
-//   -> combine (bf16) -> O GEMV (epilogue: +residual) -> rmsnorm
-//   -> gate/up GEMV (epilogue: SwiGLU, bf16) -> down GEMV (+residual)
-// and the whole step (every layer, LM head, argmax, position update) is
-// captured once into a HIP graph that reads the position and token from
-// device memory, so each token is one graph launch with no host round trip.
+// Per layer the step is five kernels:
+//   QKV GEMV (prologue: RMSNorm; epilogue: RoPE, f16 K/V append)
+//   -> split attention (last chunk per head merges, bf16 out)
+//   -> O GEMV (epilogue: +residual, tile sums of squares)
+//   -> gate/up GEMV (prologue: RMSNorm; epilogue: SwiGLU, bf16)
+//   -> down GEMV (epilogue: +residual, tile sums of squares)
+// plus the embedding and an LM-head GEMV whose epilogue takes the argmax.
+// The whole step is captured once into a HIP graph that reads the position
+// and token from device memory: one graph launch per token, no host round
+// trip.
 #include <vector>
 
 #include "attention.hpp"
@@ -29,7 +32,7 @@ enum : int { T_WQ = 0, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_ATTN_NORM, T_FFN_NO
              T_EMBED = 10, T_FINAL_NORM, T_LM_HEAD, T_KCACHE = 20, T_VCACHE };
 
 constexpr float Q4_SMIN = 0.002f, Q4_SMAX = 0.01f, NORM_STD = 0.02f;
-constexpr int ATTN_CHUNK = 64;
+constexpr int ATTN_SUBS_ENGINE = 2;  // 128 cache positions per attention split
 
 // state[0] = position, state[1] = current token, state[2] = steps taken
 struct LlamaState { int pos, token, step, pad; };
@@ -38,34 +41,31 @@ struct LlamaState { int pos, token, step, pad; };
 // kernels
 // ---------------------------------------------------------------------------
 
+// Embedding row copy (cpu.rs:151-168) into the f32 residual, plus the
+// per-16-element sums of squares the next RMSNorm prologue consumes.
 __global__ void llama_embed_kernel(const uint16_t* __restrict__ embed, const LlamaState* __restrict__ st, int d,
-                                   float* __restrict__ x) {
-    const size_t base = (size_t)st->token * d;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
-        x[i] = __uint_as_float((uint32_t)embed[base + i] << 16);
-}
-
-// rms_norm (cpu.rs:126-149) of the f32 residual with bf16 weights, written
-// as the bf16 input of the next linear.
-__global__ __launch_bounds__(256) void llama_rmsnorm_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
-                                                            int d, float eps, uint16_t* __restrict__ out) {
-    __shared__ float red[256];
+                                   float* __restrict__ x, float* __restrict__ ssq) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t * 16 >= d) return;
+    const uint16_t* src = embed + (size_t)st->token * d + t * 16;
     float s = 0.0f;
-    for (int i = threadIdx.x; i < d; i += 256) s += x[i] * x[i];
-    s = block_sum_256(s, red);
-    const float inv = 1.0f / sqrtf(s / (float)d + eps);
-    for (int i = threadIdx.x; i < d; i += 256)
-        out[i] = f32_to_bf16_rne(x[i] * inv * __uint_as_float((uint32_t)w[i] << 16));
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float v = __uint_as_float((uint32_t)src[i] << 16);
+        x[t * 16 + i] = v;
+        s += v * v;
+    }
+    ssq[t] = s;
 }
 
 // QKV epilogue: rows [0,qd) are q, [qd,qd+kvd) k, then v.  q and k get the
 // interleaved RoPE of device.rs:582-610 at the device-side position; k and v
 // are appended to the f16 cache row `pos`.
-struct EpiQKV {
+struct EpiQKV : EpiNoFinish {
     float* q; _Float16* kc; _Float16* vc;
     const float* cs; const float* sn; const LlamaState* st;
     int qd, kvd, hd;
-    __device__ __forceinline__ void operator()(int, int n, float v, const float* tile) const {
+    __device__ __forceinline__ void operator()(int, int n, float v, const float* tile, float*) const {
         const int pos = st->pos;
         const int rr = n & 15;
         float out = v;
@@ -87,45 +87,113 @@ struct EpiQKV {
     }
 };
 
-// y += linear (residual add, device.rs:721 on the f32 stream)
-struct EpiAddTo {
-    float* x;
-    __device__ __forceinline__ void operator()(int, int n, float v, const float*) const { x[n] = x[n] + v; }
+// x += linear (residual add, device.rs:721, on the f32 stream) and the tile's
+// sum of squares of the new x for the next RMSNorm prologue.
+struct EpiAddToSsq {
+    static constexpr bool HAS_FINISH = true;
+    float* x; float* ssq;
+    __device__ __forceinline__ void operator()(int, int n, float v, const float*, float* aux) const {
+        const float xn = x[n] + v;
+        x[n] = xn;
+        aux[n & 15] = xn;
+    }
+    __device__ __forceinline__ void finish(int t, int, const float* aux, int tid) const {
+        if (tid == 0) {
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) s += aux[i] * aux[i];
+            ssq[t] = s;
+        }
+    }
 };
 
 // Gate/up tiles hold gate rows 8b..8b+7 then up rows 8b..8b+7: the first
 // eight lanes emit bf16(swiglu(g, u)) for intermediate index 8b + rr.
-struct EpiSwiGLU {
+struct EpiSwiGLU : EpiNoFinish {
     uint16_t* out;
-    __device__ __forceinline__ void operator()(int, int n, float v, const float* tile) const {
+    __device__ __forceinline__ void operator()(int, int n, float v, const float* tile, float*) const {
         const int rr = n & 15;
         if (rr < 8) out[(n >> 4) * 8 + rr] = f32_to_bf16_rne(swiglu_f64(v, tile[rr + 8]));
     }
 };
 
-// Greedy argmax of the logits, then advance the position.
-__global__ __launch_bounds__(256) void llama_argmax_kernel(const float* __restrict__ logits, int vocab, LlamaState* st,
-                                                           int32_t* __restrict__ history) {
-    __shared__ float rv[256];
-    __shared__ int ri[256];
-    float bv; int bi;
-    argmax_block_256(logits, vocab, rv, ri, bv, bi);
-    if (threadIdx.x == 0) {
-        history[st->step] = bi;
-        st->token = bi;
+// LM head: store the logits and each tile's first maximum (tile order and
+// in-tile order keep sampling.rs:184-194's first-index tie rule).
+struct EpiTileMax {
+    static constexpr bool HAS_FINISH = true;
+    float* logits; float* part_v; int* part_i; int vocab;
+    __device__ __forceinline__ void operator()(int, int n, float v, const float*, float* aux) const {
+        logits[n] = v;
+        aux[n & 15] = v;
+    }
+    __device__ __forceinline__ void finish(int t, int, const float* aux, int tid) const {
+        if (tid == 0) {
+            const int cnt = min(16, vocab - t * 16);
+            float bv = -INFINITY;
+            int bi = t * 16;
+            for (int i = 0; i < cnt; i++)
+                if (aux[i] > bv) { bv = aux[i]; bi = t * 16 + i; }
+            part_v[t] = bv;
+            part_i[t] = bi;
+        }
+    }
+};
+
+// Greedy argmax over the tile maxima (first maximum wins), record the token,
+// advance the position.
+__global__ __launch_bounds__(1024) void llama_argmax_kernel(const float* __restrict__ part_v,
+                                                            const int* __restrict__ part_i, int ntile, LlamaState* st,
+                                                            int32_t* __restrict__ history) {
+    __shared__ float rv[1024];
+    __shared__ int ri[1024];
+    const int tid = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < ntile; i += 1024) {
+        const float pv = part_v[i];
+        if (pv > bv) { bv = pv; bi = part_i[i]; }
+    }
+    rv[tid] = bv;
+    ri[tid] = bi;
+    __syncthreads();
+    for (int s = 512; s > 0; s >>= 1) {
+        if (tid < s) {
+            const float ov = rv[tid + s];
+            const int oi = ri[tid + s];
+            if (ov > rv[tid] || (ov == rv[tid] && oi < ri[tid])) { rv[tid] = ov; ri[tid] = oi; }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const int tok = ri[0] == 0x7fffffff ? 0 : ri[0];
+        history[st->step] = tok;
+        st->token = tok;
         st->step += 1;
         st->pos += 1;
     }
 }
 
-template <typename Epi>
-static void gemv_bf16(const th_qweight* w, const uint16_t* x, Epi epi, hipStream_t s) {
+// One M=1 int4 GEMV of the engine: bf16 input (or the f32 residual through
+// the RMSNorm prologue when norm.ssq is set).  Small matrices split K over
+// eight waves per tile to keep enough weight bytes in flight.
+template <bool NORM, typename Epi>
+static void gemv_engine(const th_qweight* w, const void* x, NormArgs norm, Epi epi, hipStream_t s) {
     TH_REQUIRE(w->bits == 4 && w->scale_dtype == TH_F16, "engine weights must be q4 with f16 scales");
-    const size_t smem = Q4GemvSmem<1>::bytes((int)(w->Kp / 128));
-    TH_REQUIRE(smem <= 48 * 1024, "engine GEMV LDS above 48 KiB");
-    hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi>), dim3((unsigned)(w->Np / 16)), dim3(256), smem, s,
-                       (const uint4*)w->data, (const _Float16*)w->scales, (const void*)x, (int)w->cols, (int)w->Kp,
-                       (int)w->rows, (int)w->cols, epi);
+    TH_REQUIRE(!NORM || (w->cols % 16 == 0 && w->cols / 16 <= 256), "RMSNorm prologue supports K <= 4096");
+    const bool small = w->Np / 16 < 512;
+    if (small) {
+        const size_t smem = Q4GemvSmem<1, 8>::bytes((int)(w->Kp / 128));
+        TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
+        hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 8, NORM>), dim3((unsigned)(w->Np / 16)),
+                           dim3(512), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
+                           (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm);
+    } else {
+        const size_t smem = Q4GemvSmem<1, 4>::bytes((int)(w->Kp / 128));
+        TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
+        hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 4, NORM>), dim3((unsigned)(w->Np / 16)),
+                           dim3(256), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
+                           (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm);
+    }
     TH_LAUNCH_CHECK();
 }
 
@@ -142,8 +210,9 @@ struct th_llama {
     uint16_t *embed = nullptr, *attn_norm = nullptr, *ffn_norm = nullptr, *final_norm = nullptr;
     _Float16 *kcache = nullptr, *vcache = nullptr;
     float *rope_cos = nullptr, *rope_sin = nullptr;
-    float *x = nullptr, *q = nullptr, *logits = nullptr, *part = nullptr;
-    uint16_t *h = nullptr, *att = nullptr, *sg = nullptr;
+    float *x = nullptr, *q = nullptr, *logits = nullptr, *part = nullptr, *ssq = nullptr, *amax_v = nullptr;
+    uint16_t *att = nullptr, *sg = nullptr;
+    int *counters = nullptr, *amax_i = nullptr;  // counters: [n_heads] attention, [n_heads] argmax
     LlamaState* st = nullptr;
     int32_t* history = nullptr;
     hipGraphExec_t graph = nullptr;
@@ -159,7 +228,8 @@ static void llama_free(th_llama* m) {
         for (th_qweight* w : *v) th_qweight_free(w);
     if (m->lm) th_qweight_free(m->lm);
     void* ptrs[] = {m->embed, m->attn_norm, m->ffn_norm, m->final_norm, m->kcache, m->vcache, m->rope_cos,
-                    m->rope_sin, m->x, m->q, m->logits, m->part, m->h, m->att, m->sg, m->st, m->history};
+                    m->rope_sin, m->x, m->q, m->logits, m->part, m->ssq, m->amax_v, m->att, m->sg, m->counters,
+                    m->amax_i, m->st, m->history};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
@@ -178,43 +248,31 @@ static void llama_enqueue_step(th_llama* m) {
     const th_llama_config& c = m->cfg;
     hipStream_t s = m->dev->stream;
     const int d = c.d_model, hd = c.head_dim;
-    hipLaunchKernelGGL(llama_embed_kernel, dim3(16), dim3(256), 0, s, m->embed, m->st, d, m->x);
+    const int nssq = d / 16;
+    hipLaunchKernelGGL(llama_embed_kernel, dim3((unsigned)ceil_div(nssq, 256)), dim3(256), 0, s, m->embed, m->st, d, m->x,
+                       m->ssq);
     TH_LAUNCH_CHECK();
     const size_t cache_layer = (size_t)c.max_seq * m->kvd;
     for (int l = 0; l < c.n_layers; l++) {
         _Float16* kc = m->kcache + l * cache_layer;
         _Float16* vc = m->vcache + l * cache_layer;
-        hipLaunchKernelGGL(llama_rmsnorm_kernel, dim3(1), dim3(256), 0, s, m->x, m->attn_norm + (size_t)l * d, d, c.eps, m->h);
-        TH_LAUNCH_CHECK();
-        gemv_bf16(m->wqkv[l], m->h, EpiQKV{m->q, kc, vc, m->rope_cos, m->rope_sin, m->st, m->qd, m->kvd, hd}, s);
-        dim3 grid((unsigned)c.n_heads, 1, (unsigned)m->n_splits);
-        switch (hd) {
-            case 64:
-                hipLaunchKernelGGL((attn_split_kernel<64, _Float16>), grid, dim3(256), 0, s, m->q, kc, vc, 0, c.n_heads,
-                                   c.n_kv_heads, ATTN_CHUNK, m->n_splits, m->part, (const int*)&m->st->pos);
-                break;
-            case 128:
-                hipLaunchKernelGGL((attn_split_kernel<128, _Float16>), grid, dim3(256), 0, s, m->q, kc, vc, 0, c.n_heads,
-                                   c.n_kv_heads, ATTN_CHUNK, m->n_splits, m->part, (const int*)&m->st->pos);
-                break;
-            default:
-                hipLaunchKernelGGL((attn_split_kernel<256, _Float16>), grid, dim3(256), 0, s, m->q, kc, vc, 0, c.n_heads,
-                                   c.n_kv_heads, ATTN_CHUNK, m->n_splits, m->part, (const int*)&m->st->pos);
-        }
-        TH_LAUNCH_CHECK();
-        hipLaunchKernelGGL(attn_combine_kernel<true>, dim3((unsigned)c.n_heads, 1), dim3(hd < 256 ? hd : 256), 0, s,
-                           m->part, c.n_heads, hd, m->n_splits, (void*)m->att);
-        TH_LAUNCH_CHECK();
-        gemv_bf16(m->wo[l], m->att, EpiAddTo{m->x}, s);
-        hipLaunchKernelGGL(llama_rmsnorm_kernel, dim3(1), dim3(256), 0, s, m->x, m->ffn_norm + (size_t)l * d, d, c.eps, m->h);
-        TH_LAUNCH_CHECK();
-        gemv_bf16(m->wgu[l], m->h, EpiSwiGLU{m->sg}, s);
-        gemv_bf16(m->wd[l], m->sg, EpiAddTo{m->x}, s);
+        NormArgs an;
+        an.ssq = m->ssq; an.nssq = nssq; an.w = m->attn_norm + (size_t)l * d; an.eps = c.eps;
+        gemv_engine<true>(m->wqkv[l], m->x, an,
+                          EpiQKV{{}, m->q, kc, vc, m->rope_cos, m->rope_sin, m->st, m->qd, m->kvd, hd}, s);
+        launch_attn_split<true>(m->q, kc, vc, true, 0, 1, c.n_heads, c.n_kv_heads, hd, ATTN_SUBS_ENGINE, m->n_splits, m->part,
+                                m->counters, (void*)m->att, (const int*)&m->st->pos, s);
+        gemv_engine<false>(m->wo[l], m->att, NormArgs{}, EpiAddToSsq{m->x, m->ssq}, s);
+        NormArgs fn;
+        fn.ssq = m->ssq; fn.nssq = nssq; fn.w = m->ffn_norm + (size_t)l * d; fn.eps = c.eps;
+        gemv_engine<true>(m->wgu[l], m->x, fn, EpiSwiGLU{{}, m->sg}, s);
+        gemv_engine<false>(m->wd[l], m->sg, NormArgs{}, EpiAddToSsq{m->x, m->ssq}, s);
     }
-    hipLaunchKernelGGL(llama_rmsnorm_kernel, dim3(1), dim3(256), 0, s, m->x, m->final_norm, d, c.eps, m->h);
-    TH_LAUNCH_CHECK();
-    gemv_bf16(m->lm, m->h, EpiStore{m->logits, c.vocab}, s);
-    hipLaunchKernelGGL(llama_argmax_kernel, dim3(1), dim3(256), 0, s, m->logits, c.vocab, m->st, m->history);
+    NormArgs fin;
+    fin.ssq = m->ssq; fin.nssq = nssq; fin.w = m->final_norm; fin.eps = c.eps;
+    gemv_engine<true>(m->lm, m->x, fin, EpiTileMax{m->logits, m->amax_v, m->amax_i, c.vocab}, s);
+    hipLaunchKernelGGL(llama_argmax_kernel, dim3(1), dim3(1024), 0, s, m->amax_v, m->amax_i,
+                       (int)ceil_div((size_t)c.vocab, 16), m->st, m->history);
     TH_LAUNCH_CHECK();
 }
 
@@ -265,7 +323,10 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
     TH_REQUIRE(c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256, "head_dim must be 64, 128 or 256");
     TH_REQUIRE(c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
     TH_REQUIRE(c.n_heads * c.head_dim == c.d_model, "n_heads*head_dim must equal d_model");
-    TH_REQUIRE(c.d_ff % 8 == 0 && c.d_model % 8 == 0, "d_model and d_ff must be multiples of 8");
+    TH_REQUIRE(c.d_ff % 8 == 0 && c.d_model % 16 == 0, "d_model must be a multiple of 16 and d_ff of 8");
+    TH_REQUIRE(c.d_model <= 4096, "the RMSNorm prologue supports d_model <= 4096");
+    TH_REQUIRE(attn_merge_lds((int)ceil_div((size_t)c.max_seq, ATTN_SUB * ATTN_SUBS_ENGINE), c.head_dim) <= 64 * 1024,
+               "max_seq too long for the attention merge");
     th_llama* m = new th_llama();
     try {
         m->dev = dev;
@@ -273,7 +334,7 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
         m->qd = c.n_heads * c.head_dim;
         m->kvd = c.n_kv_heads * c.head_dim;
         m->max_steps = c.max_seq;
-        m->n_splits = (int)ceil_div((size_t)c.max_seq, ATTN_CHUNK);
+        m->n_splits = (int)ceil_div((size_t)c.max_seq, ATTN_SUB * ATTN_SUBS_ENGINE);
         TH_HIP(hipSetDevice(dev->ordinal));
         const size_t L = c.n_layers, d = c.d_model;
         m->embed = dalloc<uint16_t>((size_t)c.vocab * d);
@@ -288,7 +349,11 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
         m->q = dalloc<float>(m->qd);
         m->logits = dalloc<float>(c.vocab);
         m->part = dalloc<float>((size_t)c.n_heads * m->n_splits * (c.head_dim + 2));
-        m->h = dalloc<uint16_t>(d);
+        m->ssq = dalloc<float>(d / 16);
+        m->amax_v = dalloc<float>(ceil_div((size_t)c.vocab, 16));
+        m->amax_i = dalloc<int>(ceil_div((size_t)c.vocab, 16));
+        m->counters = dalloc<int>(2 * (size_t)c.n_heads + 2);
+        TH_HIP(hipMemset(m->counters, 0, (2 * (size_t)c.n_heads + 2) * sizeof(int)));
         m->att = dalloc<uint16_t>(m->qd);
         m->sg = dalloc<uint16_t>(c.d_ff);
         m->st = dalloc<LlamaState>(1);

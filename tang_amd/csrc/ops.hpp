@@ -19,6 +19,40 @@ __device__ __forceinline__ float load_w(const void* w, int bf16, size_t i) {
     return bf16 ? __uint_as_float((uint32_t)((const uint16_t*)w)[i] << 16) : ((const float*)w)[i];
 }
 
+// Cross-workgroup hand-off without cache flushes: values another workgroup
+// (possibly on another XCD, whose L2 is not coherent with ours) will read are
+// stored and loaded as relaxed device-scope atomics, which go to the
+// coherence point; an agent-scope fence would instead write back or
+// invalidate the whole L2.  wait_stores() drains this thread's stores before
+// it publishes an arrival count.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_coherent(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+// Count this workgroup's arrival; true in the last of `total` to arrive
+// (which also resets the counter).  Call with the whole block after every
+// thread's st_coherent stores.
+__device__ __forceinline__ bool last_arrival(int* counter, int total, int* s_flag) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = prev == total - 1;
+        if (*s_flag) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}
+
 // Wave-level sum: row-local DPP-free butterfly over 64 lanes.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -29,13 +29,22 @@ static bool x_vec_ok(const void* x, size_t ldx, size_t K) {
 template <int M, bool XF32, typename ST, bool VEC>
 static void q4_gemv_launch_v(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
     constexpr int MR = XF32 ? 2 * M : M;
-    const size_t smem = Q4GemvSmem<MR>::bytes((int)(w->Kp / 128));
-    TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
-    auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore>;
-    set_smem(k, smem);
     EpiStore epi{y, (int)ldy};
-    hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
-                       (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi);
+    if (w->Np / 16 < 512) {  // few tiles: split K over eight waves per tile
+        const size_t smem = Q4GemvSmem<MR, 8>::bytes((int)(w->Kp / 128));
+        TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
+        auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 8>;
+        set_smem(k, smem);
+        hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(512), smem, s, (const uint4*)w->data,
+                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{});
+    } else {
+        const size_t smem = Q4GemvSmem<MR, 4>::bytes((int)(w->Kp / 128));
+        TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
+        auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 4>;
+        set_smem(k, smem);
+        hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
+                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{});
+    }
     TH_LAUNCH_CHECK();
 }
 

@@ -77,6 +77,13 @@ __device__ __forceinline__ uint4 ldg_stream(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Sum over the 64 lanes in a fixed butterfly order (every lane gets it).
+__device__ __forceinline__ float wave_sum_fixed(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum_xor16_32(float v) {
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
@@ -91,10 +98,12 @@ __device__ __forceinline__ float wave_sum_xor16_32(float v) {
 // batch row m (tile[n % 16] == v), so an epilogue can combine neighbouring
 // output rows (RoPE pairs, gate/up halves).
 struct EpiStore {
+    static constexpr bool HAS_FINISH = false;
     float* y; int ldy;
-    __device__ __forceinline__ void operator()(int m, int n, float v, const float* tile) const {
+    __device__ __forceinline__ void operator()(int m, int n, float v, const float* tile, float*) const {
         y[(size_t)m * ldy + n] = v;
     }
+    __device__ __forceinline__ void finish(int, int, const float*, int) const {}
 };
 
 // ---------------------------------------------------------------------------
@@ -186,38 +195,70 @@ inline size_t q4_scale_count(bool f16, size_t NT, size_t GQ) {
 }
 
 // LDS bytes of the MFMA GEMV: per wave, x as [item][j][MR][q] 16-byte
-// chunks plus a zero chunk, and the bias as [item][j][8] floats.
-template <int MR>
+// chunks plus a zero chunk and the bias as [item][j][8] floats; then the
+// cross-wave reduction [NW][8][16], the finished tile [M][16] and 16 floats
+// of epilogue scratch.
+template <int MR, int NW = 4>
 struct Q4GemvSmem {
     __host__ __device__ static size_t per_wave(int items) { return (size_t)items * 4 * (MR * 64 + 32) + 16; }
     static size_t bytes(int GQ) {
-        const int items = (GQ + 3) / 4;
-        return 4 * per_wave(items) + 4 * 8 * 16 * 4 + 16 * 4 * 4;
+        const int items = (GQ + NW - 1) / NW;
+        return NW * per_wave(items) + NW * 8 * 16 * 4 + 16 * 4 * 4 + 16 * 4;
     }
 };
 
-// Scale access for one 16-byte scale record per lane: f16 holds two items
-// (u even/odd halves), f32 one item.
-template <typename ST>
+// Scale access: f16 scales of the items (gq, gq+4) share one 16-byte record,
+// so with four waves per tile one load serves two consecutive items; with
+// eight waves each item loads its own 8-byte half.
+template <typename ST, int NW>
 struct ScaleRec;
 template <>
-struct ScaleRec<_Float16> {
+struct ScaleRec<_Float16, 4> {
     static constexpr int ITEMS = 2;
-    __device__ __forceinline__ static float get(const uint4& v, int h, int j) {
+    typedef uint4 Rec;
+    __device__ __forceinline__ static float get(const Rec& v, int h, int j) {
         const uint32_t w = h ? (j < 2 ? v.z : v.w) : (j < 2 ? v.x : v.y);
         const uint16_t b = (j & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFF);
         return (float)__builtin_bit_cast(_Float16, b);
     }
 };
 template <>
-struct ScaleRec<float> {
+struct ScaleRec<_Float16, 8> {
     static constexpr int ITEMS = 1;
-    __device__ __forceinline__ static float get(const uint4& v, int, int j) {
+    typedef uint2 Rec;
+    __device__ __forceinline__ static float get(const Rec& v, int, int j) {
+        const uint32_t w = j < 2 ? v.x : v.y;
+        const uint16_t b = (j & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFF);
+        return (float)__builtin_bit_cast(_Float16, b);
+    }
+};
+template <int NW>
+struct ScaleRec<float, NW> {
+    static constexpr int ITEMS = 1;
+    typedef uint4 Rec;
+    __device__ __forceinline__ static float get(const Rec& v, int, int j) {
         return __uint_as_float(j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w);
     }
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// Optional RMSNorm prologue (rms_norm, crates/tang-compute/src/cpu.rs:126):
+// the activation is the f32 residual x; the kernel sums the producer's
+// per-16-element partials ssq[0..nssq) in a fixed order, and stages
+// bf16(x * (1/sqrt(sum/K + eps)) * w) as the linear's input.
+struct NormArgs {
+    const float* ssq = nullptr;
+    int nssq = 0;
+    const uint16_t* w = nullptr;
+    float eps = 0.0f;
+};
+
+// Default epilogue hook run by every thread after the tile's epilogue calls.
+struct EpiNoFinish {
+    static constexpr bool HAS_FINISH = false;
+    __device__ __forceinline__ void finish(int, int, const float*, int) const {}
+};
 
 // ---------------------------------------------------------------------------
 // int4 GEMV for m <= 4 on MFMA, "transposed": A = activations (row m = batch
@@ -226,71 +267,102 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 // v_mfma_f32_16x16x32_bf16 per group of 32: B holds 128+nibble as bf16
 // (exact), C carries bias = -136 * sum(x over the group) so
 // D[m][n] = sum (nibble-8) * x, and acc[m][n] += scale[n][g] * D[m][n].
-// One workgroup = one 16-row tile; wave w takes group-quads gq = w + 4i
-// ("items"), stages only the activations it needs in its own LDS region
-// (no workgroup barrier) and keeps D group-quads of weights in flight.
+// One workgroup = one 16-row tile; its NW waves take group-quads
+// gq = w + NW*i ("items"), stage only the activations they need in their own
+// LDS region (no workgroup barrier) and keep D items of weights in flight.
 // ---------------------------------------------------------------------------
-template <int MR, bool XF32, bool VEC, typename ST, typename Epi, int D = 2, int WPE = 4>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemv_kernel(const uint4* __restrict__ wt,
-                                                      const ST* __restrict__ sc,
-                                                      const void* __restrict__ xin, int K, int Kp,
-                                                      int N, int ldx, Epi epi) {
-    // D: items in flight per wave (rolling prefetch); WPE: occupancy target
-    constexpr int SI = ScaleRec<ST>::ITEMS;
-    constexpr int NS = D / SI;    // scale records in flight
+template <int MR, bool XF32, bool VEC, typename ST, typename Epi, int D = 2, int WPE = 4, int NW = 4,
+          bool NORM = false>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemv_kernel(
+    const uint4* __restrict__ wt, const ST* __restrict__ sc, const void* __restrict__ xin, int K, int Kp, int N,
+    int ldx, Epi epi, NormArgs norm) {
+    using SR = ScaleRec<ST, NW>;
+    constexpr int SI = SR::ITEMS;
+    constexpr int NS = D / SI;             // scale records in flight
     constexpr int M = XF32 ? MR / 2 : MR;  // activation rows
     constexpr bool F16S = std::is_same<ST, _Float16>::value;
+    constexpr bool LOADF32 = XF32 || NORM;
+    static_assert(!NORM || (MR == 1 && !XF32), "the RMSNorm prologue serves one bf16 row");
+    static_assert(D % SI == 0, "prefetch depth must cover whole scale records");
     extern __shared__ uint4 smem[];
     const int GQ = Kp >> 7;
-    const int items_max = (GQ + 3) >> 2;
+    const int items_max = (GQ + NW - 1) / NW;
 
     const int t = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
-    const int nmine = (GQ - wave + 3) >> 2;  // items of this wave (wave-uniform)
+    const int nmine = (GQ - wave + NW - 1) / NW;  // items of this wave (wave-uniform)
 
     // per-wave LDS region
-    char* wl = (char*)smem + (size_t)wave * Q4GemvSmem<MR>::per_wave(items_max);
+    char* wl = (char*)smem + (size_t)wave * Q4GemvSmem<MR, NW>::per_wave(items_max);
     uint4* xw = (uint4*)wl;                                   // [item][j][MR][4]
     uint4* zero = xw + (size_t)items_max * 4 * MR * 4;        // one zero chunk
     float* bw = (float*)(zero + 1);                           // [item][j][8]
-    float* red = (float*)((char*)smem + 4 * Q4GemvSmem<MR>::per_wave(items_max));  // [4][8][16]
+    float* red = (float*)((char*)smem + NW * Q4GemvSmem<MR, NW>::per_wave(items_max));  // [NW][8][16]
+    float* tilev = red + NW * 8 * 16;                         // [M][16]
+    float* aux = tilev + 16 * 4;                              // [16]
 
     const uint4* wp = wt + (size_t)t * GQ * 64 + lane;
-    auto item_off = [&](int i) { return (size_t)(i < nmine ? wave + 4 * i : 0) * 64; };
-    auto scale_ptr = [&](int i) -> const uint4* {
-        const int gq = i < nmine ? wave + 4 * i : 0;  // past the end: a valid record of this tile
-        return (const uint4*)(sc + q4_scale_index(F16S, t, F16S ? (gq & ~4) : gq, r, 0, GQ));
+    auto item_gq = [&](int i) { return i < nmine ? wave + NW * i : 0; };
+    auto scale_ptr = [&](int i) -> const typename SR::Rec* {
+        const int gq = item_gq(i);  // past the end: a valid record of this tile
+        const int g0 = (F16S && NW == 4) ? (gq & ~4) : gq;
+        return (const typename SR::Rec*)(sc + q4_scale_index(F16S, t, g0, r, 0, GQ));
     };
 
     // 1. activations for this wave's groups: task (item i, group j, row m)
     //    covers 32 values (4 chunks); a lane takes up to TPL tasks.
-    constexpr int TPL = 2;
+    constexpr int TPL = MR <= 1 ? 1 : 2;
     const int ntask = nmine * 4 * M;
-    uint4 xa[TPL][4], xb[TPL][4];
+    uint4 xa[TPL][4], xb[TPL][4], nw[TPL][4];
+    // RMSNorm partials (at most 256 = 4 per lane): loaded now, summed after
+    // the weight stream is issued.
+    float ssq_raw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (NORM) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = lane + 64 * u;
+            ssq_raw[u] = norm.ssq[i < norm.nssq ? i : 0];
+        }
+    }
 #pragma unroll
     for (int tt = 0; tt < TPL; tt++) {
         int task = lane + tt * 64;
         task = task < ntask ? task : 0;
         const int m = task % M, ij = task / M, i = ij >> 2, j = ij & 3;
-        const int g = 4 * (wave + 4 * i) + j;
+        const int g = 4 * (wave + NW * i) + j;
 #pragma unroll
-        for (int c = 0; c < 4; c++) load_x8<XF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, xa[tt][c], xb[tt][c]);
+        for (int c = 0; c < 4; c++) {
+            load_x8<LOADF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, xa[tt][c], xb[tt][c]);
+            if (NORM) {
+                uint4 dummy;
+                load_x8<false, VEC>(norm.w, 0, 0, K, g * 32 + c * 8, nw[tt][c], dummy);
+            }
+        }
     }
     // 2. weights and scales in flight
-    uint4 wbuf[D], sbuf[NS];
+    uint4 wbuf[D];
+    typename SR::Rec sbuf[NS];
 #pragma unroll
-    for (int u = 0; u < D; u++) wbuf[u] = ldg_stream(wp + item_off(u));
+    for (int u = 0; u < D; u++) wbuf[u] = ldg_stream(wp + (size_t)item_gq(u) * 64);
 #pragma unroll
     for (int v = 0; v < NS; v++) sbuf[v] = *scale_ptr(v * SI);
+    float inv_rms = 1.0f;
+    if (NORM) {
+        float part = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; u++) part += (lane + 64 * u < norm.nssq) ? ssq_raw[u] : 0.0f;
+        const float tot = wave_sum_fixed(part);
+        inv_rms = 1.0f / sqrtf(tot / (float)K + norm.eps);
+    }
     // 3. stage: bf16 pairs in nibble-pair order; f32 input as hi/lo rows
-    auto stage = [&](int task, const uint4* ra, const uint4* rb) {
+    auto stage = [&](int task, const uint4* ra, const uint4* rb, const uint4* rw) {
         const int m = task % M, ij = task / M;
         float s_hi = 0.0f, s_lo = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             float xv[8];
-            if (XF32) {
+            if (LOADF32) {
                 xv[0] = __uint_as_float(ra[c].x); xv[1] = __uint_as_float(ra[c].y);
                 xv[2] = __uint_as_float(ra[c].z); xv[3] = __uint_as_float(ra[c].w);
                 xv[4] = __uint_as_float(rb[c].x); xv[5] = __uint_as_float(rb[c].y);
@@ -301,6 +373,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
                 for (int e = 0; e < 4; e++) {
                     xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
                     xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
+                }
+            }
+            if (NORM) {
+                const uint32_t w4[4] = {rw[c].x, rw[c].y, rw[c].z, rw[c].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    // cpu.rs:146: x * inv_rms * w
+                    xv[2 * e] = xv[2 * e] * inv_rms * bf16_bits_to_f32(w4[e] & 0xFFFF);
+                    xv[2 * e + 1] = xv[2 * e + 1] * inv_rms * bf16_bits_to_f32(w4[e] >> 16);
                 }
             }
             uint32_t hi[8], lo[8];
@@ -334,15 +415,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
 #pragma unroll
     for (int tt = 0; tt < TPL; tt++) {
         const int task = lane + tt * 64;
-        if (task < ntask) stage(task, xa[tt], xb[tt]);
+        if (task < ntask) stage(task, xa[tt], xb[tt], nw[tt]);
     }
     for (int task = lane + TPL * 64; task < ntask; task += 64) {
-        uint4 ra[4], rb[4];
+        uint4 ra[4], rb[4], rw[4];
         const int m = task % M, ij = task / M, i = ij >> 2, j = ij & 3;
-        const int g = 4 * (wave + 4 * i) + j;
+        const int g = 4 * (wave + NW * i) + j;
 #pragma unroll
-        for (int c = 0; c < 4; c++) load_x8<XF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, ra[c], rb[c]);
-        stage(task, ra, rb);
+        for (int c = 0; c < 4; c++) {
+            load_x8<LOADF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, ra[c], rb[c]);
+            if (NORM) {
+                uint4 dummy;
+                load_x8<false, VEC>(norm.w, 0, 0, K, g * 32 + c * 8, rw[c], dummy);
+            }
+        }
+        stage(task, ra, rb, rw);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -361,12 +448,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
         const bool valid = i < nmine;
         const int ii = valid ? i : 0;
         const uint4 wv = wbuf[u];
-        const uint4 sv = sbuf[u / SI];
+        const typename SR::Rec sv = sbuf[u / SI];
         float sj[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) sj[j] = valid ? ScaleRec<ST>::get(sv, u % SI, j) : 0.0f;
+        for (int j = 0; j < 4; j++) sj[j] = valid ? SR::get(sv, u % SI, j) : 0.0f;
         if constexpr (decltype(refill_tag)::value) {
-            wbuf[u] = ldg_stream(wp + item_off(i + D));
+            wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
             if (u % SI == SI - 1) sbuf[u / SI] = *scale_ptr(i + D - (SI - 1));
         }
         const uint32_t wj[4] = {wv.x, wv.y, wv.z, wv.w};
@@ -409,17 +496,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
             if (4 * q + e < MR) red[(wave * 8 + 4 * q + e) * 16 + r] = acc[e];
     }
     __syncthreads();
-    float* tilev = red + 4 * 8 * 16;  // [M][16]
     float v = 0.0f;
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
-        if (XF32) {
 #pragma unroll
-            for (int w = 0; w < 4; w++) v += red[(w * 8 + 2 * m) * 16 + rr] + red[(w * 8 + 2 * m + 1) * 16 + rr];
-        } else {
-            v = red[(0 * 8 + m) * 16 + rr] + red[(1 * 8 + m) * 16 + rr];
-            v += red[(2 * 8 + m) * 16 + rr];
-            v += red[(3 * 8 + m) * 16 + rr];
+        for (int w = 0; w < NW; w++) {
+            if (XF32) v += red[(w * 8 + 2 * m) * 16 + rr] + red[(w * 8 + 2 * m + 1) * 16 + rr];
+            else v += red[(w * 8 + m) * 16 + rr];
         }
         tilev[m * 16 + rr] = v;
     }
@@ -427,7 +510,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
         const int n = t * 16 + rr;
-        if (n < N) epi(m, n, v, tilev + m * 16);
+        if (n < N) epi(m, n, v, tilev + m * 16, aux);
+    }
+    if constexpr (Epi::HAS_FINISH) {
+        __syncthreads();
+        epi.finish(t, (int)gridDim.x, aux, tid);
     }
 }
 
@@ -440,7 +527,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) void
 
 template <int M>
 struct Q8GemvSmem {
-    static size_t bytes(int Kp) { return (size_t)M * Kp * 4 + (size_t)M * (Kp / 16) * 4 + 5 * 16 * M * 4; }
+    static size_t bytes(int Kp) { return (size_t)M * Kp * 4 + (size_t)M * (Kp / 16) * 4 + 5 * 16 * M * 4 + 64 * 4; }
 };
 
 template <int M, bool XF32, bool VEC, bool PER_ROW, typename Epi>
@@ -581,7 +668,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
         const int n = t * 16 + rr;
-        if (n < N) epi(m, n, v, tilev + m * 16);
+        if (n < N) epi(m, n, v, tilev + m * 16, tilev + 4 * 16);
     }
 }
 

@@ -15,7 +15,14 @@ sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
 from llama_ref import CONFIG_7B, OracleLlama  # noqa: E402
 
-SEED, KV_SEED, PREFILL, FIRST_TOKEN, STEPS = 3, 33, 2048, 1, 128
+# FIRST_TOKEN: greedy decoding from a random-init model meets near-ties (a
+# top-2 logit gap comparable to the f32-vs-f64 rounding of two correct
+# implementations; with first token 1 the gap at step 59 is 1.3e-5 and the
+# token there depends on summation order).  Token 10 was chosen by scanning
+# first tokens 1..40 on the device for the largest minimum top-2 gap among
+# trajectories that visit more than one token (min gap 9.1e-5, 3 distinct
+# tokens); the gaps of every step are stored with the tokens.
+SEED, KV_SEED, PREFILL, FIRST_TOKEN, STEPS = 3, 33, 2048, 10, 128
 
 
 def main():
