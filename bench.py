@@ -30,6 +30,9 @@ PEAK_HBM_GBS = 8000.0
 N, K = 11008, 4096
 GEMV_BYTES = {1: 25414656, 4: 25571328, 8: 25780224, 16: 26198016}  # algorithmic bytes per call
 N_COPIES = 12  # 12 x 25.4 MB = 305 MB > 256 MB last-level cache
+# HBM bytes per M=1 launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE runs in
+# profiles/q4_gemv_config2.md, each scaled by its reading of a known-size copy.
+TRAFFIC_BYTES = 25549700
 
 CFG7B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=32, head_dim=128, d_ff=11008, vocab=32000,
              max_seq=2176, eps=1e-5, rope_theta=1e4)
@@ -117,6 +120,8 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-gemv", action="store_true",
+                    help="counter runs: 240 GEMV launches, then one 256 MiB device copy as the traffic calibration")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (collectives are out of scope); "
@@ -124,6 +129,13 @@ def main():
         sys.exit(2)
 
     dev = capi.HipComputeDevice(0)
+    if args.profile_gemv:
+        gemv_bench(dev, 1, 240, 0)
+        a, b = dev.alloc(256 << 20, capi.U8), dev.alloc(256 << 20, capi.U8)
+        capi.check(capi.lib().th_buffer_copy(b.handle, a.handle))
+        dev.sync()
+        print(json.dumps({"profile_gemv": True, "launches": 240, "copy_bytes": 256 << 20}))
+        return
     ms = gemv_bench(dev, 1, args.steps, args.warmup)
     us = ms * 1e3 / args.steps
     gbs = GEMV_BYTES[1] / us / 1e3
@@ -152,7 +164,8 @@ def main():
                                "%d rotating weight copies (305 MB > 256 MB MALL)" % N_COPIES,
                    "M_sweep": extra},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES,
+                     "traffic_source": "profiles/q4_gemv_config2.md (FETCH_SIZE/WRITE_SIZE, copy-calibrated)"},
         "cpu_baseline": cpu,
         "decode_7b": decode,
     }

@@ -83,6 +83,10 @@ int th_buffer_download(th_buffer* buf, void* host, size_t n);
 int th_buffer_info(const th_buffer* buf, th_dtype* dtype, size_t* n);
 /* ComputeDevice::zero_buffer. */
 int th_buffer_zero(th_buffer* buf);
+/* Device-to-device copy of min(src, dst) bytes on the device stream
+ * (ComputeDevice::copy_buffer-style helper; also the known-size copy the
+ * HBM-traffic counters are calibrated against). */
+int th_buffer_copy(th_buffer* dst, const th_buffer* src);
 /* Element-wise dtype conversion between f32, bf16 and f16 buffers of equal
  * length; f32->bf16 rounds as crates/tang-compute/src/cuda.rs:22-27,
  * f32->f16 is IEEE round-to-nearest-even (kernels BF16_TO_F32_CUDA /

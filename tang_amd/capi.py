@@ -58,6 +58,7 @@ SIGNATURES = {
     "th_buffer_download": ([_P, _P, _S], _I),
     "th_buffer_info": ([_P, _P, _P], _I),
     "th_buffer_zero": ([_P], _I),
+    "th_buffer_copy": ([_P, _P], _I),
     "th_convert": ([_P, _P, _P], _I),
     "th_q4_upload_blocks": ([_P, _P, _S, _S, _I, _P], _I),
     "th_q4_upload_packed": ([_P, _P, _P, _I, _S, _S, _P], _I),

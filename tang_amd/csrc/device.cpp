@@ -315,6 +315,14 @@ int th_buffer_download(th_buffer* b, void* host, size_t n) {
     TH_API_END
 }
 
+int th_buffer_copy(th_buffer* dst, const th_buffer* src) {
+    TH_API_BEGIN
+    TH_REQUIRE(dst && src && dst->dev == src->dev, "buffers must share a device");
+    const size_t bytes = std::min(dst->n * dtype_size(dst->dtype), src->n * dtype_size(src->dtype));
+    if (bytes) TH_HIP(hipMemcpyAsync(dst->ptr, src->ptr, bytes, hipMemcpyDeviceToDevice, dst->dev->stream));
+    TH_API_END
+}
+
 int th_buffer_info(const th_buffer* b, th_dtype* dt, size_t* n) {
     TH_API_BEGIN
     TH_REQUIRE(b, "null buffer");
