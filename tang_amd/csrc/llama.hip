@@ -186,13 +186,13 @@ static void gemv_engine(const th_qweight* w, const void* x, NormArgs norm, Epi e
         TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
         hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 8, NORM>), dim3((unsigned)(w->Np / 16)),
                            dim3(512), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
-                           (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm);
+                           (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm, SingleMatrix{});
     } else {
         const size_t smem = Q4GemvSmem<1, 4>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
         hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 4, NORM>), dim3((unsigned)(w->Np / 16)),
                            dim3(256), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
-                           (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm);
+                           (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm, SingleMatrix{});
     }
     TH_LAUNCH_CHECK();
 }

@@ -36,14 +36,14 @@ static void q4_gemv_launch_v(const th_qweight* w, const void* x, size_t ldx, flo
         auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 8>;
         set_smem(k, smem);
         hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(512), smem, s, (const uint4*)w->data,
-                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{});
+                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, SingleMatrix{});
     } else {
         const size_t smem = Q4GemvSmem<MR, 4>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
         auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 4>;
         set_smem(k, smem);
         hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
-                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{});
+                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, SingleMatrix{});
     }
     TH_LAUNCH_CHECK();
 }

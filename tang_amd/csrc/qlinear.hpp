@@ -200,11 +200,28 @@ inline size_t q4_scale_count(bool f16, size_t NT, size_t GQ) {
 // of epilogue scratch.
 template <int MR, int NW = 4>
 struct Q4GemvSmem {
-    __host__ __device__ static size_t per_wave(int items) { return (size_t)items * 4 * (MR * 64 + 32) + 16; }
+    static constexpr int BS = MR <= 8 ? 8 : 16;  // bias floats per (item, group)
+    static constexpr int RS = MR <= 8 ? 8 : 16;  // reduction rows
+    __host__ __device__ static size_t per_wave(int items) { return (size_t)items * 4 * (MR * 64 + BS * 4) + 16; }
     static size_t bytes(int GQ) {
         const int items = (GQ + NW - 1) / NW;
-        return NW * per_wave(items) + NW * 8 * 16 * 4 + 16 * 4 * 4 + 16 * 4;
+        return NW * per_wave(items) + NW * RS * 16 * 4 + 16 * 16 * 4 + 16 * 4;
     }
+};
+
+// Default source of a GEMV workgroup: one weight matrix, tile = blockIdx.x,
+// activation rows 0..M-1.  A grouped launch (MoE experts) supplies a policy
+// with the same members that picks the expert's weights, the tile, the
+// number of live rows and the gathered activation / output rows.
+struct SingleMatrix {
+    static constexpr bool GROUPED = false;
+    template <typename ST>
+    __device__ __forceinline__ bool select(int bid, const uint4*& wt, const ST*& sc, int& t, int& mrows) {
+        t = bid;
+        return true;
+    }
+    __device__ __forceinline__ int x_row(int m) const { return m; }
+    __device__ __forceinline__ int out_row(int m) const { return m; }
 };
 
 // Scale access: f16 scales of the items (gq, gq+4) share one 16-byte record,
@@ -272,10 +289,10 @@ struct EpiNoFinish {
 // LDS region (no workgroup barrier) and keep D items of weights in flight.
 // ---------------------------------------------------------------------------
 template <int MR, bool XF32, bool VEC, typename ST, typename Epi, int D = 2, int WPE = 4, int NW = 4,
-          bool NORM = false>
+          bool NORM = false, typename Src = SingleMatrix>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemv_kernel(
     const uint4* __restrict__ wt, const ST* __restrict__ sc, const void* __restrict__ xin, int K, int Kp, int N,
-    int ldx, Epi epi, NormArgs norm) {
+    int ldx, Epi epi, NormArgs norm, Src src = Src{}) {
     using SR = ScaleRec<ST, NW>;
     constexpr int SI = SR::ITEMS;
     constexpr int NS = D / SI;             // scale records in flight
@@ -284,11 +301,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     constexpr bool LOADF32 = XF32 || NORM;
     static_assert(!NORM || (MR == 1 && !XF32), "the RMSNorm prologue serves one bf16 row");
     static_assert(D % SI == 0, "prefetch depth must cover whole scale records");
+    constexpr int BS = Q4GemvSmem<MR, NW>::BS, RS = Q4GemvSmem<MR, NW>::RS;
     extern __shared__ uint4 smem[];
     const int GQ = Kp >> 7;
     const int items_max = (GQ + NW - 1) / NW;
 
-    const int t = blockIdx.x;
+    int t = 0, mrows = M;  // tile, live activation rows (<= M)
+    {
+        const uint4* wsel = wt;
+        const ST* ssel = sc;
+        if (!src.select((int)blockIdx.x, wsel, ssel, t, mrows)) return;
+        wt = wsel;
+        sc = ssel;
+    }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
     const int nmine = (GQ - wave + NW - 1) / NW;  // items of this wave (wave-uniform)
@@ -297,10 +322,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     char* wl = (char*)smem + (size_t)wave * Q4GemvSmem<MR, NW>::per_wave(items_max);
     uint4* xw = (uint4*)wl;                                   // [item][j][MR][4]
     uint4* zero = xw + (size_t)items_max * 4 * MR * 4;        // one zero chunk
-    float* bw = (float*)(zero + 1);                           // [item][j][8]
-    float* red = (float*)((char*)smem + NW * Q4GemvSmem<MR, NW>::per_wave(items_max));  // [NW][8][16]
-    float* tilev = red + NW * 8 * 16;                         // [M][16]
-    float* aux = tilev + 16 * 4;                              // [16]
+    float* bw = (float*)(zero + 1);                           // [item][j][BS]
+    float* red = (float*)((char*)smem + NW * Q4GemvSmem<MR, NW>::per_wave(items_max));  // [NW][RS][16]
+    float* tilev = red + NW * RS * 16;                        // [M][16]
+    float* aux = tilev + 16 * 16;                             // [16]
 
     const uint4* wp = wt + (size_t)t * GQ * 64 + lane;
     auto item_gq = [&](int i) { return i < nmine ? wave + NW * i : 0; };
@@ -313,7 +338,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     // 1. activations for this wave's groups: task (item i, group j, row m)
     //    covers 32 values (4 chunks); a lane takes up to TPL tasks.
     constexpr int TPL = MR <= 1 ? 1 : 2;
-    const int ntask = nmine * 4 * M;
+    const int ntask = nmine * 4 * mrows;
     uint4 xa[TPL][4], xb[TPL][4], nw[TPL][4];
     // RMSNorm partials (at most 256 = 4 per lane): loaded now, summed after
     // the weight stream is issued.
@@ -329,11 +354,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     for (int tt = 0; tt < TPL; tt++) {
         int task = lane + tt * 64;
         task = task < ntask ? task : 0;
-        const int m = task % M, ij = task / M, i = ij >> 2, j = ij & 3;
+        const int m = task % mrows, ij = task / mrows, i = ij >> 2, j = ij & 3;
         const int g = 4 * (wave + NW * i) + j;
+        const int xr = src.x_row(m);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            load_x8<LOADF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, xa[tt][c], xb[tt][c]);
+            load_x8<LOADF32, VEC>(xin, xr, ldx, K, g * 32 + c * 8, xa[tt][c], xb[tt][c]);
             if (NORM) {
                 uint4 dummy;
                 load_x8<false, VEC>(norm.w, 0, 0, K, g * 32 + c * 8, nw[tt][c], dummy);
@@ -357,7 +383,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     }
     // 3. stage: bf16 pairs in nibble-pair order; f32 input as hi/lo rows
     auto stage = [&](int task, const uint4* ra, const uint4* rb, const uint4* rw) {
-        const int m = task % M, ij = task / M;
+        const int m = task % mrows, ij = task / mrows;
         float s_hi = 0.0f, s_lo = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -403,15 +429,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
             }
         }
         if (XF32) {
-            bw[ij * 8 + 2 * m] = -136.0f * s_hi;
-            bw[ij * 8 + 2 * m + 1] = -136.0f * s_lo;
+            bw[ij * BS + 2 * m] = -136.0f * s_hi;
+            bw[ij * BS + 2 * m + 1] = -136.0f * s_lo;
         } else {
-            bw[ij * 8 + m] = -136.0f * s_hi;
+            bw[ij * BS + m] = -136.0f * s_hi;
         }
     };
     if (lane == 0) *zero = make_uint4(0, 0, 0, 0);
+    const int mr_live = XF32 ? 2 * mrows : mrows;
     for (int ij = lane; ij < nmine * 4; ij += 64)
-        for (int e = MR; e < 8; e++) bw[ij * 8 + e] = 0.0f;
+        for (int e = mr_live; e < BS; e++) bw[ij * BS + e] = 0.0f;
 #pragma unroll
     for (int tt = 0; tt < TPL; tt++) {
         const int task = lane + tt * 64;
@@ -419,11 +446,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     }
     for (int task = lane + TPL * 64; task < ntask; task += 64) {
         uint4 ra[4], rb[4], rw[4];
-        const int m = task % M, ij = task / M, i = ij >> 2, j = ij & 3;
+        const int m = task % mrows, ij = task / mrows, i = ij >> 2, j = ij & 3;
         const int g = 4 * (wave + NW * i) + j;
+        const int xr = src.x_row(m);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            load_x8<LOADF32, VEC>(xin, m, ldx, K, g * 32 + c * 8, ra[c], rb[c]);
+            load_x8<LOADF32, VEC>(xin, xr, ldx, K, g * 32 + c * 8, ra[c], rb[c]);
             if (NORM) {
                 uint4 dummy;
                 load_x8<false, VEC>(norm.w, 0, 0, K, g * 32 + c * 8, rw[c], dummy);
@@ -439,8 +467,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     constexpr int ACC = MR < 4 ? MR : 4;
     // A rows >= MR and C rows >= MR only feed D rows that are discarded, so
     // those lanes read real (finite) data of another row: no masking needed.
-    const uint4* abase = xw + (size_t)(r < MR ? r : 0) * 4 + q;
-    const float* cbase = bw + 4 * (q & 1);
+    const uint4* abase = xw + (size_t)(r < mr_live ? r : 0) * 4 + q;
+    const float* cbase = bw + 4 * (q & (BS / 4 - 1));
     float4_t dprev = {0.0f, 0.0f, 0.0f, 0.0f};
     float sprev = 0.0f;
 
@@ -458,14 +486,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         }
         const uint32_t wj[4] = {wv.x, wv.y, wv.z, wv.w};
         const uint4* ai = abase + (size_t)ii * 4 * MR * 4;
-        const float* ci = cbase + ii * 32;
+        const float* ci = cbase + ii * 4 * BS;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             uint32_t p[4];
             nib_pairs_perm(wj[j], p);
             const uint4 bq = make_uint4(p[0], p[1], p[2], p[3]);
             const uint4 aq = ai[j * MR * 4];
-            const float4 cb = *(const float4*)(ci + j * 8);
+            const float4 cb = *(const float4*)(ci + j * BS);
             const float4_t c = {cb.x, cb.y, cb.z, cb.w};
             const float4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                 __builtin_bit_cast(bf16x8_t, aq), __builtin_bit_cast(bf16x8_t, bq), c, 0, 0, 0);
@@ -493,7 +521,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     if (q * 4 < MR) {
 #pragma unroll
         for (int e = 0; e < ACC; e++)
-            if (4 * q + e < MR) red[(wave * 8 + 4 * q + e) * 16 + r] = acc[e];
+            if (4 * q + e < MR) red[(wave * RS + 4 * q + e) * 16 + r] = acc[e];
     }
     __syncthreads();
     float v = 0.0f;
@@ -501,8 +529,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         const int m = tid >> 4, rr = tid & 15;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            if (XF32) v += red[(w * 8 + 2 * m) * 16 + rr] + red[(w * 8 + 2 * m + 1) * 16 + rr];
-            else v += red[(w * 8 + m) * 16 + rr];
+            if (XF32) v += red[(w * RS + 2 * m) * 16 + rr] + red[(w * RS + 2 * m + 1) * 16 + rr];
+            else v += red[(w * RS + m) * 16 + rr];
         }
         tilev[m * 16 + rr] = v;
     }
@@ -510,7 +538,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
         const int n = t * 16 + rr;
-        if (n < N) epi(m, n, v, tilev + m * 16, aux);
+        if (n < N && m < mrows) epi(src.out_row(m), n, v, tilev + m * 16, aux);
     }
     if constexpr (Epi::HAS_FINISH) {
         __syncthreads();
