@@ -259,3 +259,19 @@ def softmax(x, rows, length):
 def argmax(x):
     x = np.ascontiguousarray(x, np.float32)
     return int(lib().or_argmax_f32(p(x), x.size))
+
+
+def mla_decode(q_nope, q_rope, cache_bf16, B, H, L, dn, dr, r, dv, wuk, wuk_scale, wuv, wuv_scale, sm_scale,
+               threads=0):
+    """Absorbed MLA decode (f64 accumulation); out f32 [B][H][dv]."""
+    q_nope = np.ascontiguousarray(q_nope, np.float32)
+    q_rope = np.ascontiguousarray(q_rope, np.float32)
+    cache_bf16 = np.ascontiguousarray(cache_bf16, np.uint16)
+    wuk = np.ascontiguousarray(wuk, np.int8)
+    wuv = np.ascontiguousarray(wuv, np.int8)
+    wuk_scale = np.ascontiguousarray(wuk_scale, np.float32)
+    wuv_scale = np.ascontiguousarray(wuv_scale, np.float32)
+    out = np.empty(B * H * dv, np.float32)
+    lib().or_mla_decode(p(q_nope), p(q_rope), p(cache_bf16), B, H, L, dn, dr, r, dv, p(wuk), p(wuk_scale), p(wuv),
+                        p(wuv_scale), float(sm_scale), p(out), threads)
+    return out

@@ -373,6 +373,14 @@ class HipComputeDevice:
         check(lib().th_argmax(self.handle, data.handle, n_rows, n, out.handle))
         return out
 
+    def mla_decode(self, q_nope, q_rope, cache, B, H, L, dn, dr, r, dv, w_uk, w_uv, sm_scale, out=None):
+        """Absorbed MLA decode: q_nope/q_rope f32, cache bf16 [B][L][r+dr],
+        w_uk/w_uv q8 rowwise; returns out f32 [B][H][dv]."""
+        out = out or self.alloc(B * H * dv)
+        check(lib().th_mla_decode(self.handle, q_nope.handle, q_rope.handle, cache.handle, B, H, L, dn, dr, r, dv,
+                                  w_uk.handle, w_uv.handle, sm_scale, out.handle))
+        return out
+
     def close(self):
         if self.handle:
             check(lib().th_device_destroy(self.handle))

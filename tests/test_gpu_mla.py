@@ -1,0 +1,63 @@
+"""MLA absorbed decode (16 heads, qk_nope 128, qk_rope 64,
+v_head 128, kv_lora_rank 512, bf16 latent cache) against the oracle's
+from-definition or_mla_decode, through the C ABI.  Activations and outputs are
+f32, so the bar is 1e-3 max-abs-rel."""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import max_abs_rel
+from tang_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+H, DN, DR, R, DV = 16, 128, 64, 512, 128
+TOL = 1e-3
+
+
+def _case(seed, B, L, dn=DN, dr=DR, r=R, dv=DV):
+    qn = capi.synth_normal(capi.synth_seed(seed, 0, 0), B * H * dn, 1.0, capi.F32)
+    qr = capi.synth_normal(capi.synth_seed(seed, 0, 1), B * H * dr, 1.0, capi.F32)
+    cache = capi.synth_normal(capi.synth_seed(seed, 0, 2), B * L * (r + dr), 1.0, capi.BF16)
+    wuk, suk = capi.synth_q8_rowwise(capi.synth_seed(seed, 0, 3), H * r, dn)
+    wuv, suv = capi.synth_q8_rowwise(capi.synth_seed(seed, 0, 4), H * dv, r)
+    return qn, qr, cache, wuk, suk, wuv, suv
+
+
+def _run(dev, B, L, seed, dn=DN, dr=DR, r=R, dv=DV):
+    qn, qr, cache, wuk, suk, wuv, suv = _case(seed, B, L, dn, dr, r, dv)
+    scale = 1.0 / np.sqrt(dn + dr)
+    ref = oracle.mla_decode(qn, qr, cache, B, H, L, dn, dr, r, dv, wuk, suk, wuv, suv, scale)
+    wk = dev.q8_upload_rowwise(wuk, suk, H * r, dn)
+    wv = dev.q8_upload_rowwise(wuv, suv, H * dv, r)
+    out = dev.mla_decode(dev.upload(qn), dev.upload(qr), dev.upload(cache, capi.BF16), B, H, L, dn, dr, r, dv,
+                         wk, wv, scale).to_numpy()
+    return out, ref
+
+
+@pytest.mark.parametrize("B,L", [(8, 4096), (1, 1), (3, 37), (2, 129), (1, 8192), (16, 200)])
+def test_mla_matches_oracle(dev, B, L):
+    print(f"mla B={B} L={L}", flush=True)
+    out, ref = _run(dev, B, L, seed=50 + L)
+    err = max_abs_rel(out, ref)
+    print("max_abs_rel", err)
+    assert np.isfinite(out).all() and err < TOL
+
+
+def test_mla_small_latent_and_repeat(dev):
+    """Other widths (r=64, dr=32, dn=48, dv=32) and two calls in a row sharing
+    the device workspace and split counters."""
+    for B, L in ((2, 300), (1, 65)):
+        out, ref = _run(dev, B, L, seed=7, dn=48, dr=32, r=64, dv=32)
+        assert max_abs_rel(out, ref) < TOL
+
+
+def test_mla_rejects_bad_shapes(dev):
+    qn, qr, cache, wuk, suk, wuv, suv = _case(1, 1, 8)
+    wk = dev.q8_upload_rowwise(wuk, suk, H * R, DN)
+    wv = dev.q8_upload_rowwise(wuv, suv, H * DV, R)
+    bq, br, bc = dev.upload(qn), dev.upload(qr), dev.upload(cache, capi.BF16)
+    with pytest.raises(capi.TangHipError):  # cache buffer too short for L
+        dev.mla_decode(bq, br, bc, 1, H, 9, DN, DR, R, DV, wk, wv, 0.1)
+    with pytest.raises(capi.TangHipError):  # w_uk / w_uv swapped
+        dev.mla_decode(bq, br, bc, 1, H, 8, DN, DR, R, DV, wv, wk, 0.1)

@@ -309,3 +309,87 @@ def test_softmax_and_argmax():
 def test_embedding_kat():  # cpu.rs:1000-1016
     out = oracle.embedding(np.array([0.1, 0.2, 0.3, 0.4, 0.5, 0.6], np.float32), [2, 0, 1], 3, 2)
     assert np.allclose(out, [0.5, 0.6, 0.1, 0.2, 0.3, 0.4])
+
+
+# ---- MoE and MLA: no reference implementation; pinned by invariants ----------
+
+def _np_dequant_q4(nib, sc, rows, cols):
+    """[rows][cols] f64 from packed nibbles (low nibble = even element) and
+    per-group scales: value = (nibble - 8) * scale."""
+    b = nib.reshape(rows, -1)
+    v = np.empty((rows, b.shape[1] * 2), np.float64)
+    v[:, 0::2] = (b & 0x0F).astype(np.int64) - 8
+    v[:, 1::2] = (b >> 4).astype(np.int64) - 8
+    v = v[:, :cols]
+    return v * np.repeat(sc.reshape(rows, -1).astype(np.float64), 32, axis=1)[:, :cols]
+
+
+def _bf16_round(x):
+    return oracle.bf16_to_f32(oracle.f32_to_bf16(np.asarray(x, np.float32))).astype(np.float64)
+
+
+@pytest.mark.parametrize("topk", [4, 2])
+def test_moe_oracle_matches_dense_mixture(topk):
+    """out = sum over the top-k experts of p_e * expert_e(h) + shared(h), with p
+    the softmax over all router logits (not renormalised) and expert_e computed
+    densely from the dequantised weights.  With top-k = E it is the full
+    softmax mixture; with top-k < E the chosen set must be the k largest p."""
+    from moe_ref import OracleMoe
+    from tang_amd import capi
+    cfg = dict(d=64, ff=96, E=4, S=1, k=topk)
+    om = OracleMoe(cfg, seed=5)
+    T = 3
+    h = capi.synth_normal(77, T * cfg["d"], 1.0, capi.BF16)
+    out, idx, w = om.forward(h, T, threads=1)
+    hf = oracle.bf16_to_f32(h).astype(np.float64).reshape(T, cfg["d"])
+    router = om.router.astype(np.float64).reshape(cfg["E"], cfg["d"])
+
+    def expert(e, x):
+        mats = []
+        for tid, rows, cols in ((4, cfg["ff"], cfg["d"]), (5, cfg["ff"], cfg["d"]), (6, cfg["d"], cfg["ff"])):
+            nib, sc16 = capi.synth_q4(capi.synth_seed(5, e, tid), rows, cols)
+            mats.append(_np_dequant_q4(nib, oracle.f16_to_f32(sc16), rows, cols))
+        g = (mats[0] @ x).astype(np.float32).astype(np.float64)
+        u = (mats[1] @ x).astype(np.float32).astype(np.float64)
+        s = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+        return (mats[2] @ _bf16_round(s)).astype(np.float32).astype(np.float64)
+
+    for t in range(T):
+        lg = router @ hf[t]
+        p = np.exp(lg - lg.max())
+        p /= p.sum()
+        order = np.argsort(-p, kind="stable")[:topk]
+        assert list(idx[t]) == list(order)
+        assert np.allclose(w[t], p[order], rtol=1e-5, atol=1e-7)
+        ref = sum(p[e] * expert(e, hf[t]) for e in order) + expert(cfg["E"], hf[t])
+        assert max_abs_rel(out[t], ref) < 1e-5
+
+
+def test_mla_oracle_matches_explicit_decompression():
+    """Absorbed decode equals attention over the decompressed cache:
+    k[t,h] = [W_UK[h]^T c_t ; kr_t], v[t,h] = W_UV[h] c_t, scores
+    (q_nope.k_nope + q_rope.kr) * scale, out = sum_t softmax(s) v."""
+    rng = np.random.default_rng(11)
+    B, H, L, dn, dr, r, dv = 2, 3, 37, 16, 8, 24, 12
+    qn = rng.standard_normal(B * H * dn).astype(np.float32)
+    qr = rng.standard_normal(B * H * dr).astype(np.float32)
+    cache = oracle.f32_to_bf16(rng.standard_normal(B * L * (r + dr)).astype(np.float32))
+    wuk = rng.integers(-127, 128, H * r * dn).astype(np.int8)
+    wuv = rng.integers(-127, 128, H * dv * r).astype(np.int8)
+    suk = rng.uniform(0.005, 0.02, H * r).astype(np.float32)
+    suv = rng.uniform(0.005, 0.02, H * dv).astype(np.float32)
+    scale = 1.0 / np.sqrt(dn + dr)
+    out = oracle.mla_decode(qn, qr, cache, B, H, L, dn, dr, r, dv, wuk, suk, wuv, suv, scale, threads=1)
+    c = oracle.bf16_to_f32(cache).astype(np.float64).reshape(B, L, r + dr)
+    Wuk = wuk.astype(np.float64).reshape(H, r, dn) * suk.reshape(H, r, 1)
+    Wuv = wuv.astype(np.float64).reshape(H, dv, r) * suv.reshape(H, dv, 1)
+    ref = np.empty((B, H, dv))
+    for b in range(B):
+        for h in range(H):
+            k_nope = c[b, :, :r] @ Wuk[h]          # [L][dn]: decompressed keys
+            v = c[b, :, :r] @ Wuv[h].T              # [L][dv]: decompressed values
+            s = (k_nope @ qn.reshape(B, H, dn)[b, h] + c[b, :, r:] @ qr.reshape(B, H, dr)[b, h]) * scale
+            pr = np.exp(s - s.max())
+            pr /= pr.sum()
+            ref[b, h] = pr @ v
+    assert max_abs_rel(out, ref.reshape(-1)) < 1e-5
