@@ -77,9 +77,9 @@ def decode_bench(dev, steps):
         capi.check(L.th_llama_fill_kv_synthetic(h, 2048, 33))
         init_s = time.time() - t0
         ms = ctypes.c_float()
-        capi.check(L.th_llama_time_steps(h, 1, 2048, 8, ctypes.byref(ms)))  # warm (graph build)
+        capi.check(L.th_llama_time_steps(h, 10, 2048, 8, ctypes.byref(ms)))  # warm (graph build)
         capi.check(L.th_llama_fill_kv_synthetic(h, 2048, 33))
-        capi.check(L.th_llama_time_steps(h, 1, 2048, steps, ctypes.byref(ms)))
+        capi.check(L.th_llama_time_steps(h, 10, 2048, steps, ctypes.byref(ms)))
     finally:
         L.th_llama_destroy(h)
     per_tok_ms = ms.value / steps
