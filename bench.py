@@ -92,6 +92,70 @@ def decode_bench(dev, steps):
                 init_s=round(init_s, 1))
 
 
+MOE = dict(d=2048, ff=1408, E=64, S=2, k=6)
+MLA = dict(B=8, H=16, L=4096, dn=128, dr=64, r=512, dv=128)
+
+
+def moe_bench(dev, T, iters):
+    """Config 4 MoE layer forward (router, dispatch, grouped int4 experts,
+    combine) on T tokens.  Algorithmic bytes: every weight byte of the experts
+    the batch routes to (+ shared experts) once, the router, h in, out."""
+    import ctypes
+    c = MOE
+    L = capi.lib()
+    h = ctypes.c_void_p()
+    capi.check(L.th_moe_create(dev.handle, c["d"], c["ff"], c["E"], c["S"], c["k"], ctypes.byref(h)))
+    try:
+        capi.check(L.th_moe_init_synthetic(h, 4))
+        x = dev.upload(capi.synth_normal(45, T * c["d"], 1.0, capi.BF16), capi.BF16)
+        out, idx, w = dev.alloc(T * c["d"]), dev.alloc(T * c["k"], capi.I32), dev.alloc(T * c["k"])
+        for _ in range(5):
+            capi.check(L.th_moe_forward(h, x.handle, T, out.handle, idx.handle, w.handle))
+        dev.sync()
+        dev.timer_start()
+        for _ in range(iters):
+            capi.check(L.th_moe_forward(h, x.handle, T, out.handle, idx.handle, w.handle))
+        ms = dev.timer_stop()
+        used = len(np.unique(idx.to_numpy())) + c["S"]
+    finally:
+        L.th_moe_destroy(h)
+    lin = 3 * c["ff"] * c["d"]
+    nbytes = used * (lin // 2 + lin // 32 * 2) + c["E"] * c["d"] * 4 + T * c["d"] * (2 + 4)
+    us = ms * 1e3 / iters
+    flops = 2 * T * (c["k"] + c["S"]) * lin
+    return dict(T=T, us=round(us, 2), experts_read=used, bytes=int(nbytes), gbs=round(nbytes / us / 1e3, 1),
+                frac_hbm=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), tflops=round(flops / us / 1e6, 2))
+
+
+def mla_bench(dev, iters, copies=8):
+    """Config 5 absorbed MLA decode, B=8 sequences x 4096 latent positions.
+    Rotates `copies` caches (8 x 37.7 MB > 256 MB MALL).  Algorithmic bytes:
+    the latent cache, W_UK and W_UV with their scales, q in, out."""
+    c = MLA
+    B, H, Lk, dn, dr, r, dv = c["B"], c["H"], c["L"], c["dn"], c["dr"], c["r"], c["dv"]
+    qn = dev.upload(capi.synth_normal(1, B * H * dn, 1.0, capi.F32))
+    qr = dev.upload(capi.synth_normal(2, B * H * dr, 1.0, capi.F32))
+    host_cache = capi.synth_normal(3, B * Lk * (r + dr), 1.0, capi.BF16)
+    caches = [dev.upload(host_cache, capi.BF16) for _ in range(copies)]
+    wuk = dev.q8_upload_rowwise(*capi.synth_q8_rowwise(4, H * r, dn), H * r, dn)
+    wuv = dev.q8_upload_rowwise(*capi.synth_q8_rowwise(5, H * dv, r), H * dv, r)
+    out = dev.alloc(B * H * dv)
+    scale = 1.0 / np.sqrt(dn + dr)
+    for i in range(copies):
+        dev.mla_decode(qn, qr, caches[i], B, H, Lk, dn, dr, r, dv, wuk, wuv, scale, out)
+    dev.sync()
+    dev.timer_start()
+    for i in range(iters):
+        dev.mla_decode(qn, qr, caches[i % copies], B, H, Lk, dn, dr, r, dv, wuk, wuv, scale, out)
+    ms = dev.timer_stop()
+    us = ms * 1e3 / iters
+    nbytes = B * Lk * (r + dr) * 2 + H * r * (dn + 4) + H * dv * (r + 4) + B * H * (dn + dr + dv) * 4
+    for b in caches:
+        b.free()
+    return dict(us=round(us, 2), bytes=int(nbytes), gbs=round(nbytes / us / 1e3, 1),
+                frac_hbm=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4))
+
+
 def cpu_baseline(budget_s=12.0):
     """Oracle q4_matvec (f64, one thread) on config-2 rows: a bounded sample."""
     import oracle
@@ -120,6 +184,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-moe-mla", action="store_true")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="counter runs: 240 GEMV launches, then one 256 MiB device copy as the traffic calibration")
     args = ap.parse_args()
@@ -146,6 +211,8 @@ def main():
         extra["M=%d" % m] = dict(us=round(usm, 3), gbs=round(GEMV_BYTES[m] / usm / 1e3, 1),
                                  frac=round(GEMV_BYTES[m] / usm / 1e3 / PEAK_HBM_GBS, 4))
     decode = None if args.no_decode else decode_bench(dev, args.decode_steps)
+    moe = None if args.no_moe_mla else [moe_bench(dev, 16, 200), moe_bench(dev, 512, 50)]
+    mla = None if args.no_moe_mla else mla_bench(dev, 400)
     cpu = None if args.no_cpu else cpu_baseline()
     out = {
         "metric": METRIC,
@@ -168,6 +235,8 @@ def main():
                      "traffic_source": "profiles/q4_gemv_config2.md (FETCH_SIZE/WRITE_SIZE, copy-calibrated)"},
         "cpu_baseline": cpu,
         "decode_7b": decode,
+        "moe_config4": moe,
+        "mla_config5": mla,
     }
     print(json.dumps(out))
     dev.close()

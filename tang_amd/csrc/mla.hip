@@ -7,15 +7,22 @@
 //   o_lat[b,h] = sum_t softmax_t(s) c[b,t,:r]
 //   out[b,h]   = W_UV[h] . o_lat[b,h]                 (int8, per-row scale)
 // Three launches:
-//   1. absorb: q_lat (f32) emitted as hi+mid+lo bf16 parts (24 significant
-//      bits; scores reach ~1e2, so a 16-bit split would cost ~1e-3), with
-//      q_rope appended, as the MFMA A operand [B][3][H][r+dr];
-//   2. one workgroup per (sequence, split of 128 positions) serves all H
-//      heads from one pass over the latent cache: the chunk is staged in LDS,
-//      scores run on v_mfma_f32_16x16x32_bf16 (heads x positions), online
-//      softmax per head, P.C on VALU; the last split of a sequence merges;
+//   1. absorb: q = [q_lat ; q_rope] (f32) emitted as hi + lo bf16 parts
+//      (16 significant bits) as the MFMA A operand [B][2][H][r+dr];
+//   2. one workgroup per (sequence, split of 128 positions) serves all 16
+//      heads from one pass over the latent cache, in chunks of 64 positions
+//      staged in LDS (the next chunk is loaded into registers meanwhile):
+//      scores on v_mfma_f32_16x16x32_bf16 (heads x positions; each wave owns
+//      a quarter of the k-steps and keeps its A operand in registers; partial
+//      scores are summed in LDS), online softmax per head, then P.C on the
+//      same MFMA (P as hi + lo bf16, C exact bf16); the per-split
+//      {max, sum, o_lat} records are then merged by a small kernel with one
+//      workgroup per (sequence, head);
 //   3. up-projection through W_UV.
 // The cache dominates the traffic: B*L*(r+dr)*2 bytes.
+#include <mutex>
+#include <utility>
+
 #include "capi_util.hpp"
 #include "ops.hpp"
 #include "qlinear.hpp"
@@ -27,67 +34,103 @@ constexpr int MLA_CHUNK = 64;   // positions staged per pass
 constexpr int MLA_SPLIT = 128;  // positions per workgroup
 
 // Per-head batched int8 GEMV over the tiled q8 layout (16 rows x 64 k per
-// tile, lane q*16+r holds k 16q..16q+15 of row r), per-row scales.
+// tile, lane q*16+r holds k 16q..16q+15 of row r), per-row scales:
 // y[b][h][n] = scale[h*rows+n] * sum_k q[h*rows+n][k] * x[b][h][k].
-// One workgroup: head h, 16 output rows, all B inputs; thread (row, b).
-template <int MODE>  // 0: absorb (write hi/mid/lo bf16 A operand), 1: plain f32 out
+// One workgroup: head h, 16 output rows, all B inputs.  Thread (row r,
+// slice kq) owns the 16-value pieces kq, kq+16, ... of its row: every weight
+// byte is loaded once, up front; partial sums meet in LDS.
+constexpr int MLA_GEMV_PIECES = 4;  // pieces per thread: K <= 1024
+constexpr int MLA_GEMV_X4 = 8;      // float4 activation loads per thread: B * K <= 8192
+
+template <int MODE>  // 0: absorb (write the hi / lo bf16 A operand), 1: plain f32 out
 __global__ __launch_bounds__(256) void mla_q8_heads_kernel(const uint8_t* __restrict__ wq, const float* __restrict__ wsc,
                                                            int rows_per_head, int K, int Kp, int B, int H,
                                                            const float* __restrict__ x, int ldx_b, int ldx_h,
                                                            float* __restrict__ y, uint16_t* __restrict__ qa,
                                                            const float* __restrict__ q_rope, int dr) {
-    extern __shared__ float xs[];  // [B][K]
+    extern __shared__ float sm[];
+    const int NP = Kp >> 4, NCH = Kp >> 6;
+    float* xs = sm;                          // [B][NP][20]: piece-major; the pad puts a wave's 4 slices in different banks
+    float* red = sm + (size_t)B * NP * 20;   // [B][16 slices][16 rows]
     const int h = blockIdx.x, t_local = blockIdx.y, tid = threadIdx.x;
-    for (int i = tid; i < B * K; i += blockDim.x) {
-        const int b = i / K, k = i - b * K;
-        xs[i] = x[(size_t)b * ldx_b + (size_t)h * ldx_h + k];
-    }
-    __syncthreads();
-    const int r = tid & 15, b = tid >> 4;
-    if (b >= B) return;
-    const int row = h * rows_per_head + t_local * 16 + r;  // global row of the stacked matrix
+    const int r = tid & 15, kq = tid >> 4;
+    const int row = h * rows_per_head + t_local * 16 + r;  // row of the stacked matrix
     const int t = row >> 4;                                // its 16-row tile
-    const int NCH = Kp >> 6;
-    float acc = 0.0f;
-    for (int c = 0; c < NCH; c++) {
+    uint4 w[MLA_GEMV_PIECES];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint4 w = *(const uint4*)(wq + (((size_t)t * NCH + c) * 64 + q * 16 + r) * 16);
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-            const int k0 = c * 64 + q * 16;
+    for (int j = 0; j < MLA_GEMV_PIECES; j++) {
+        const int p = min(kq + 16 * j, NP - 1);  // surplus pieces: loaded, not used
+        w[j] = *(const uint4*)(wq + (((size_t)t * NCH + (p >> 2)) * 64 + (p & 3) * 16 + r) * 16);
+    }
+    const float sc = wsc[row];
+    // activations: float4 pieces, every load issued before any is used (a
+    // loop of load-then-store would wait out one latency per iteration);
+    // surplus threads repeat the last piece, k >= K is zero
+    {
+        const int K4 = Kp >> 2, n4 = B * K4;
+        float4 xv[MLA_GEMV_X4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+        for (int u = 0; u < MLA_GEMV_X4; u++) {
+            const int i = min(tid + 256 * u, n4 - 1);
+            const int b = i / K4, k = (i - b * K4) * 4;
+            xv[u] = *(const float4*)(x + (size_t)b * ldx_b + (size_t)h * ldx_h + min(k, K - 4));
+            if (k >= K) xv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int k = k0 + j * 4 + e;
-                    const float xv = k < K ? xs[b * K + k] : 0.0f;
-                    acc = __builtin_fmaf((float)(int8_t)(ww[j] >> (8 * e)), xv, acc);
-                }
-            }
+        for (int u = 0; u < MLA_GEMV_X4; u++) {
+            const int i = min(tid + 256 * u, n4 - 1);
+            const int b = i / K4, k = (i - b * K4) * 4;
+            *(float4*)(xs + (b * NP + (k >> 4)) * 20 + (k & 15)) = xv[u];
         }
     }
-    const float v = acc * wsc[row];
+    // weights as f32 once (surplus pieces contribute zero)
+    float wf[MLA_GEMV_PIECES][16];
+#pragma unroll
+    for (int j = 0; j < MLA_GEMV_PIECES; j++) {
+        const bool live = kq + 16 * j < NP;
+        const uint32_t wj[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+        for (int e = 0; e < 16; e++) wf[j][e] = live ? (float)(int8_t)(wj[e >> 2] >> (8 * (e & 3))) : 0.0f;
+    }
+    __syncthreads();
+    for (int b = 0; b < B; b++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MLA_GEMV_PIECES; j++) {
+            const float4* xp = (const float4*)(xs + (b * NP + min(kq + 16 * j, NP - 1)) * 20);
+#pragma unroll
+            for (int e4 = 0; e4 < 4; e4++) {
+                const float4 xv = xp[e4];
+                acc = __builtin_fmaf(wf[j][4 * e4], xv.x, acc);
+                acc = __builtin_fmaf(wf[j][4 * e4 + 1], xv.y, acc);
+                acc = __builtin_fmaf(wf[j][4 * e4 + 2], xv.z, acc);
+                acc = __builtin_fmaf(wf[j][4 * e4 + 3], xv.w, acc);
+            }
+        }
+        red[(b * 16 + kq) * 16 + r] = acc;
+    }
+    __syncthreads();
+    if (tid >= 16 * B) return;
+    const int b = tid >> 4;  // r = tid & 15 as above
+    float v = 0.0f;
+#pragma unroll
+    for (int k2 = 0; k2 < 16; k2++) v += red[(b * 16 + k2) * 16 + r];
+    v *= sc;
     const int n = t_local * 16 + r;
     if (MODE == 0) {
-        // A operand row (b, part, h): q_lat parts then q_rope parts
+        // A operand row (b, part, h): q_lat then q_rope, as hi / lo parts
         const int R = rows_per_head, W = R + dr;
         const uint32_t hi = f32_to_bf16_bits(v);
-        const float r1 = v - bf16_bits_to_f32(hi);
-        const uint32_t mid = f32_to_bf16_bits(r1);
-        const uint32_t lo = f32_to_bf16_bits(r1 - bf16_bits_to_f32(mid));
-        qa[(((size_t)b * 3 + 0) * H + h) * W + n] = (uint16_t)hi;
-        qa[(((size_t)b * 3 + 1) * H + h) * W + n] = (uint16_t)mid;
-        qa[(((size_t)b * 3 + 2) * H + h) * W + n] = (uint16_t)lo;
+        const uint32_t lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
+        qa[(((size_t)b * 2 + 0) * H + h) * W + n] = (uint16_t)hi;
+        qa[(((size_t)b * 2 + 1) * H + h) * W + n] = (uint16_t)lo;
         if (t_local == 0) {
             for (int i = r; i < dr; i += 16) {
                 const float qr = q_rope[((size_t)b * H + h) * dr + i];
                 const uint32_t h2 = f32_to_bf16_bits(qr);
-                const float s1 = qr - bf16_bits_to_f32(h2);
-                const uint32_t m2 = f32_to_bf16_bits(s1);
-                const uint32_t l2 = f32_to_bf16_bits(s1 - bf16_bits_to_f32(m2));
-                qa[(((size_t)b * 3 + 0) * H + h) * W + R + i] = (uint16_t)h2;
-                qa[(((size_t)b * 3 + 1) * H + h) * W + R + i] = (uint16_t)m2;
-                qa[(((size_t)b * 3 + 2) * H + h) * W + R + i] = (uint16_t)l2;
+                const uint32_t l2 = f32_to_bf16_bits(qr - bf16_bits_to_f32(h2));
+                qa[(((size_t)b * 2 + 0) * H + h) * W + R + i] = (uint16_t)h2;
+                qa[(((size_t)b * 2 + 1) * H + h) * W + R + i] = (uint16_t)l2;
             }
         }
     } else {
@@ -96,142 +139,284 @@ __global__ __launch_bounds__(256) void mla_q8_heads_kernel(const uint8_t* __rest
 }
 
 // Latent attention for one (sequence b, split s of MLA_SPLIT positions), all
-// H = 16 heads.  W = r + dr (576) columns per cache row.  Each wave scores 16
-// positions of a 64-position chunk: D[head][pos] = sum_k A[head][k] B[k][pos]
-// over W/32 k-steps x 3 parts (hi, mid, lo).  Record per (b, s, h):
-// {m, l, acc[r]} (coherent stores); the last split of b merges into o_lat.
-__global__ __launch_bounds__(256) void mla_attn_kernel(const uint16_t* __restrict__ qa, const uint16_t* __restrict__ cache,
-                                                       int L, int R, int dr, float sm_scale, int n_splits,
-                                                       float* __restrict__ part, int* __restrict__ counters,
-                                                       float* __restrict__ o_lat) {
+// 16 heads.  W = r + dr columns per cache row (W % 32 == 0, W <= 576); cache
+// rows sit in LDS at a stride of W + 8 bf16 so that the 16 rows one score
+// MFMA reads start in different banks.  Record per (b, s, h): {m, l, acc[r]},
+// with acc unnormalised (sum of p * c with p = exp(s - m)).
+constexpr int MLA_WMAX = 576;
+constexpr int MLA_WAVES = 8;                                 // 512 threads, two waves per SIMD
+constexpr int MLA_THREADS = 64 * MLA_WAVES;
+constexpr int MLA_NT = 512 / 16 / MLA_WAVES;                 // P.C output tiles of 16 latent dims per wave
+
+// W = r + dr is a template parameter (a multiple of 32 up to 576) so that
+// every index below is a constant expression.
+template <int W>
+__global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* __restrict__ qa,
+                                                               const uint16_t* __restrict__ cache, int L, int R,
+                                                               float sm_scale, int n_splits, float* __restrict__ part) {
+    constexpr int WP = W + 8, KS = W / 32, PR = W / 8;  // PR: 16-byte pieces per row
+    constexpr int KSW = (KS + MLA_WAVES - 1) / MLA_WAVES;  // k-steps per wave
+    constexpr int pieces = MLA_CHUNK * PR;
+    constexpr int PPT = (pieces + MLA_THREADS - 1) / MLA_THREADS;  // pieces per thread
     extern __shared__ uint4 lds_raw[];
-    const int W = R + dr;
-    uint16_t* cs = (uint16_t*)lds_raw;                           // [MLA_CHUNK][W] bf16
-    float* ps = (float*)(cs + (size_t)MLA_CHUNK * W);            // [MLA_H][MLA_CHUNK] probabilities
-    float* mrow = ps + MLA_H * MLA_CHUNK;                        // [4 waves][MLA_H] chunk maxima
-    __shared__ float m_run[MLA_H], l_run[MLA_H], rescale[MLA_H];
-    __shared__ int s_last;
+    uint16_t* cs = (uint16_t*)lds_raw;                         // [MLA_CHUNK][WP]
+    float* sred = (float*)(cs + (size_t)MLA_CHUNK * WP);        // [MLA_WAVES][MLA_H][MLA_CHUNK] partial scores
+    float* ps = sred + MLA_WAVES * MLA_H * MLA_CHUNK;           // [MLA_H][MLA_PS] probabilities
+    constexpr int MLA_PS = MLA_CHUNK + 1;                       // odd stride: the 16 heads in different banks
+    __shared__ float m_run[MLA_H], l_run[MLA_H], resc[MLA_H];
     const int b = blockIdx.x, s = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
     const int p0 = s * MLA_SPLIT;
-    const int len = max(0, min(MLA_SPLIT, L - p0));
+    const int len = min(MLA_SPLIT, L - p0);  // >= 1: the grid has ceil(L / MLA_SPLIT) splits
+    const int nch = (len + MLA_CHUNK - 1) / MLA_CHUNK;
     const uint16_t* cb = cache + (size_t)b * L * W;
-    // accumulators: thread owns latent dims d = tid, tid + 256 (R <= 512) for all heads
-    constexpr int DPT = 2;
-    float acc[MLA_H][DPT];
+
+    // A operand of this wave's k-steps (ks = wave + 8 i), hi and lo parts;
+    // k-steps past W read a valid row and are multiplied by zero.
+    uint4 areg[KSW][2];
+    const uint16_t* qab = qa + (size_t)b * 2 * MLA_H * W;
 #pragma unroll
-    for (int hh = 0; hh < MLA_H; hh++)
+    for (int i = 0; i < KSW; i++) {
+        const int ks = min(wave + MLA_WAVES * i, KS - 1);
+        const bool live = wave + MLA_WAVES * i < KS;
 #pragma unroll
-        for (int i = 0; i < DPT; i++) acc[hh][i] = 0.0f;
+        for (int pp = 0; pp < 2; pp++) {
+            const uint4 v = *(const uint4*)(qab + ((size_t)pp * MLA_H + r) * W + ks * 32 + q * 8);
+            areg[i][pp] = make_uint4(live ? v.x : 0u, live ? v.y : 0u, live ? v.z : 0u, live ? v.w : 0u);
+        }
+    }
+    // this thread's pieces: row offset within a chunk and column (fixed)
+    int prow[PPT], pcol[PPT];
+#pragma unroll
+    for (int u = 0; u < PPT; u++) {
+        const int i = min(tid + MLA_THREADS * u, pieces - 1);
+        prow[u] = i / PR;
+        pcol[u] = (i - prow[u] * PR) * 8;
+    }
+    const int last = p0 + len - 1;  // rows past the split are clamped here and masked below
+    u32x4_t pre[PPT];  // native vectors: an array of uint4 structs stays in scratch memory
+#pragma unroll
+    for (int u = 0; u < PPT; u++) pre[u] = *(const u32x4_t*)(cb + (size_t)min(p0 + prow[u], last) * W + pcol[u]);
+    float4_t acc[MLA_NT];
+#pragma unroll
+    for (int nt = 0; nt < MLA_NT; nt++) acc[nt] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
     if (tid < MLA_H) { m_run[tid] = -INFINITY; l_run[tid] = 0.0f; }
-    const uint16_t* qab = qa + (size_t)b * 3 * MLA_H * W;
-    for (int c0 = 0; c0 < len; c0 += MLA_CHUNK) {
-        const int clen = min(MLA_CHUNK, len - c0);
-        // stage the chunk (16-byte pieces; W*2 is a multiple of 16)
-        const int pieces = MLA_CHUNK * W / 8;
-        for (int i = tid; i < pieces; i += 256) {
-            const int pos = i / (W / 8), col = (i - pos * (W / 8)) * 8;
-            const int src = pos < clen ? p0 + c0 + pos : p0 + c0;  // clamp: masked below
-            *(uint4*)(cs + (size_t)pos * W + col) = *(const uint4*)(cb + (size_t)src * W + col);
-        }
-        __syncthreads();
-        // scores: wave handles positions 16*wave .. +15
-        float4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
-        const int pos_b = wave * 16 + r;  // B column owned by this lane
-        for (int k0 = 0; k0 < W; k0 += 32) {
-            const uint4 bq = *(const uint4*)(cs + (size_t)pos_b * W + k0 + q * 8);
+
+    for (int c = 0; c < nch; c++) {
+        const int clen = min(MLA_CHUNK, len - c * MLA_CHUNK);
+        // branch-free (a load under a branch makes the compiler wait for
+        // every load in flight): surplus pieces rewrite the last piece with
+        // its own value, and the last chunk "prefetches" itself (L2 hits)
 #pragma unroll
-            for (int part = 0; part < 3; part++) {
-                const uint4 aq = *(const uint4*)(qab + ((size_t)part * MLA_H + r) * W + k0 + q * 8);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, aq),
-                                                            __builtin_bit_cast(bf16x8_t, bq), d, 0, 0, 0);
+        for (int u = 0; u < PPT; u++) *(u32x4_t*)(cs + (size_t)prow[u] * WP + pcol[u]) = pre[u];
+        __syncthreads();
+        {
+            const int cn = p0 + min(c + 1, nch - 1) * MLA_CHUNK;
+#pragma unroll
+            for (int u = 0; u < PPT; u++) pre[u] = *(const u32x4_t*)(cb + (size_t)min(cn + prow[u], last) * W + pcol[u]);
+        }
+        // partial scores over this wave's k-steps: D[head][position]
+        float4_t d[4];
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) d[pt] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < KSW; i++) {
+            const int ks = min(wave + MLA_WAVES * i, KS - 1);
+            uint4 bq[4];
+#pragma unroll
+            for (int pt = 0; pt < 4; pt++) bq[pt] = *(const uint4*)(cs + (size_t)(pt * 16 + r) * WP + ks * 32 + q * 8);
+#pragma unroll
+            for (int pp = 0; pp < 2; pp++)
+#pragma unroll
+                for (int pt = 0; pt < 4; pt++)
+                    d[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, areg[i][pp]),
+                                                                    __builtin_bit_cast(bf16x8_t, bq[pt]), d[pt], 0, 0, 0);
+        }
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) sred[(wave * MLA_H + 4 * q + j) * MLA_CHUNK + pt * 16 + r] = d[pt][j];
+        __syncthreads();
+        // softmax step: thread (head hh, positions 2 pg, 2 pg + 1); 32 threads per head
+        {
+            const int hh = tid >> 5, pg = tid & 31;
+            float sv[2];
+            float cmax = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int p = 2 * pg + j;
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < MLA_WAVES; w++) v += sred[(w * MLA_H + hh) * MLA_CHUNK + p];
+                sv[j] = p < clen ? v * sm_scale : -INFINITY;
+                cmax = fmaxf(cmax, sv[j]);
+            }
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, o, 64));
+            const float mold = m_run[hh];
+            const float mnew = fmaxf(mold, cmax);
+            float lsum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const float e = 2 * pg + j < clen ? expf(sv[j] - mnew) : 0.0f;
+                ps[hh * MLA_PS + 2 * pg + j] = e;
+                lsum += e;
+            }
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
+            __syncthreads();  // every thread has read m_run
+            if (pg == 0) {
+                const float f = expf(mold - mnew);
+                resc[hh] = f;
+                l_run[hh] = l_run[hh] * f + lsum;
+                m_run[hh] = mnew;
             }
         }
-        // lane (q, r) holds D[head 4q+i][position 16*wave + r]
-        float sc4[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) sc4[i] = (16 * wave + r < clen) ? d[i] * sm_scale : -INFINITY;
-        // per-head max over this wave's 16 positions, then over the 4 waves
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float mx = sc4[i];
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-            if (r == 0) mrow[wave * MLA_H + 4 * q + i] = mx;
-        }
         __syncthreads();
-        if (tid < MLA_H) {
-            float mx = fmaxf(fmaxf(mrow[tid], mrow[MLA_H + tid]), fmaxf(mrow[2 * MLA_H + tid], mrow[3 * MLA_H + tid]));
-            const float mn = fmaxf(m_run[tid], mx);
-            rescale[tid] = expf(m_run[tid] - mn);
-            m_run[tid] = mn;
+        // P.C: D[head][latent dim] += P[head][pos] C[pos][dim].  MFMA k index
+        // 8q + j of step kk stands for position 8j + 2q + kk: the four lane
+        // groups then read cache rows 2 apart (8 banks apart), not 8 apart.
+        uint4 ahi[2], alo[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            float pv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) pv[j] = ps[r * MLA_PS + 8 * j + 2 * q + kk];
+            uint32_t h2[4], l2[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t ha = f32_to_bf16_bits(pv[2 * e]), hb = f32_to_bf16_bits(pv[2 * e + 1]);
+                const uint32_t la = f32_to_bf16_bits(pv[2 * e] - bf16_bits_to_f32(ha));
+                const uint32_t lb = f32_to_bf16_bits(pv[2 * e + 1] - bf16_bits_to_f32(hb));
+                h2[e] = ha | (hb << 16);
+                l2[e] = la | (lb << 16);
+            }
+            ahi[kk] = make_uint4(h2[0], h2[1], h2[2], h2[3]);
+            alo[kk] = make_uint4(l2[0], l2[1], l2[2], l2[3]);
         }
-        __syncthreads();
+        float f4[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int hh = 4 * q + i;
-            ps[hh * MLA_CHUNK + 16 * wave + r] = (16 * wave + r < clen) ? expf(sc4[i] - m_run[hh]) : 0.0f;
-        }
-        __syncthreads();
-        if (tid < MLA_H) {
-            float l = 0.0f;
-            for (int p = 0; p < clen; p++) l += ps[tid * MLA_CHUNK + p];
-            l_run[tid] = l_run[tid] * rescale[tid] + l;
-        }
-        // P.C for this thread's latent dims
+        for (int j = 0; j < 4; j++) f4[j] = resc[4 * q + j];
+        uint4 bq[MLA_NT][2];
 #pragma unroll
-        for (int i = 0; i < DPT; i++) {
-            const int dd = tid + 256 * i;
-            if (dd < R) {
+        for (int nt = 0; nt < MLA_NT; nt++) {
+            const int d0 = min((wave * MLA_NT + nt) * 16, R - 16);  // tiles past r: computed, not stored
 #pragma unroll
-                for (int hh = 0; hh < MLA_H; hh++) acc[hh][i] *= rescale[hh];
-                for (int p = 0; p < clen; p++) {
-                    const float cv = __uint_as_float((uint32_t)cs[(size_t)p * W + dd] << 16);
+            for (int kk = 0; kk < 2; kk++) {
+                uint32_t bw[4];
 #pragma unroll
-                    for (int hh = 0; hh < MLA_H; hh++) acc[hh][i] = __builtin_fmaf(ps[hh * MLA_CHUNK + p], cv, acc[hh][i]);
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t x0 = cs[(size_t)(16 * e + 2 * q + kk) * WP + d0 + r];
+                    const uint32_t x1 = cs[(size_t)(16 * e + 8 + 2 * q + kk) * WP + d0 + r];
+                    bw[e] = x0 | (x1 << 16);
                 }
+                bq[nt][kk] = make_uint4(bw[0], bw[1], bw[2], bw[3]);
             }
         }
-        __syncthreads();  // cs/ps reused by the next chunk
-    }
-    // record per head: {m, l, acc[R]}
-    float* recs = part + (size_t)b * n_splits * MLA_H * (R + 2);
-    float* rec = recs + (size_t)s * MLA_H * (R + 2);
 #pragma unroll
-    for (int i = 0; i < DPT; i++) {
-        const int dd = tid + 256 * i;
-        if (dd < R)
+        for (int nt = 0; nt < MLA_NT; nt++) {
 #pragma unroll
-            for (int hh = 0; hh < MLA_H; hh++) st_coherent(&rec[(size_t)hh * (R + 2) + 2 + dd], acc[hh][i]);
-    }
-    if (tid < MLA_H) {
-        st_coherent(&rec[(size_t)tid * (R + 2)], len > 0 ? m_run[tid] : -INFINITY);
-        st_coherent(&rec[(size_t)tid * (R + 2) + 1], l_run[tid]);
-    }
-    if (!last_arrival(&counters[b], n_splits, &s_last)) return;
-    // merge splits of sequence b (split order), per head
-    __shared__ float wts[MLA_H][64];
-    __shared__ float Ls[MLA_H];
-    if (tid < MLA_H) {
-        float M = -INFINITY;
-        for (int sp = 0; sp < n_splits; sp++) M = fmaxf(M, ld_coherent(&recs[((size_t)sp * MLA_H + tid) * (R + 2)]));
-        float Lsum = 0.0f;
-        for (int sp = 0; sp < n_splits; sp++) {
-            const float m = ld_coherent(&recs[((size_t)sp * MLA_H + tid) * (R + 2)]);
-            const float w = m == -INFINITY ? 0.0f : expf(m - M);
-            wts[tid][sp] = w;
-            Lsum += w * ld_coherent(&recs[((size_t)sp * MLA_H + tid) * (R + 2) + 1]);
+            for (int j = 0; j < 4; j++) acc[nt][j] *= f4[j];
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ahi[kk]),
+                                                                  __builtin_bit_cast(bf16x8_t, bq[nt][kk]), acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, alo[kk]),
+                                                                  __builtin_bit_cast(bf16x8_t, bq[nt][kk]), acc[nt], 0, 0, 0);
+            }
         }
-        Ls[tid] = Lsum;
+        __syncthreads();  // cs, sred and ps are rewritten by the next chunk
+    }
+    // record per head: {m, l, acc[R]}; lane (q, r) holds heads 4q..4q+3 of dim d0 + r
+    // (plain stores: the merge is the next launch)
+    float* rec = part + ((size_t)b * n_splits + s) * MLA_H * (R + 2);
+#pragma unroll
+    for (int nt = 0; nt < MLA_NT; nt++) {
+        const int d0 = (wave * MLA_NT + nt) * 16;
+        if (d0 < R)
+#pragma unroll
+            for (int j = 0; j < 4; j++) rec[(size_t)(4 * q + j) * (R + 2) + 2 + d0 + r] = acc[nt][j];
+    }
+    if (tid < MLA_H) {
+        rec[(size_t)tid * (R + 2)] = m_run[tid];
+        rec[(size_t)tid * (R + 2) + 1] = l_run[tid];
+    }
+}
+
+// o_lat[b][h] = sum_s w_s acc_s / sum_s w_s l_s with w_s = exp(m_s - max m).
+// Workgroup (sequence, head, 128 latent dims); thread (dim, quarter of the
+// splits), quarters summed in order.
+__global__ __launch_bounds__(512) void mla_merge_kernel(const float* __restrict__ part, int n_splits, int R,
+                                                        float* __restrict__ o_lat) {
+    __shared__ float wts[64];
+    __shared__ float Lsh;
+    __shared__ float sum4[4][128];
+    const int b = blockIdx.x, hh = blockIdx.y, tid = threadIdx.x;
+    const int d = blockIdx.z * 128 + (tid & 127), g = tid >> 7;
+    const float* recs = part + (size_t)b * n_splits * MLA_H * (R + 2);
+    const int per = (n_splits + 3) / 4, s0 = g * per, s1 = min(n_splits, s0 + per);
+    const int dd = min(d, R - 1);
+    float v[16];  // issued before the (dependent) max / sum phase
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = recs[((size_t)min(s0 + i, n_splits - 1) * MLA_H + hh) * (R + 2) + 2 + dd];
+    if (tid < 64) {
+        const float* rec = recs + ((size_t)min(tid, n_splits - 1) * MLA_H + hh) * (R + 2);
+        const float m = tid < n_splits ? rec[0] : -INFINITY;
+        const float l = tid < n_splits ? rec[1] : 0.0f;
+        float M = m;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float w = tid < n_splits ? expf(m - M) : 0.0f;
+        const float L = wave_sum(w * l);
+        wts[tid] = w;
+        if (tid == 0) Lsh = L;
     }
     __syncthreads();
-    for (int i = tid; i < MLA_H * R; i += 256) {
-        const int hh = i / R, dd = i - hh * R;
-        float a = 0.0f;
-        for (int sp = 0; sp < n_splits; sp++) a += ld_coherent(&recs[((size_t)sp * MLA_H + hh) * (R + 2) + 2 + dd]) * wts[hh][sp];
-        o_lat[((size_t)b * MLA_H + hh) * R + dd] = a / Ls[hh];
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) a += s0 + i < s1 ? v[i] * wts[s0 + i] : 0.0f;
+    sum4[g][tid & 127] = a;
+    __syncthreads();
+    if (g == 0 && d < R)
+        o_lat[((size_t)b * MLA_H + hh) * R + d] =
+            (((sum4[0][tid] + sum4[1][tid]) + sum4[2][tid]) + sum4[3][tid]) / Lsh;
+}
+
+static size_t head_gemv_lds(size_t B, size_t Kp) { return (B * (Kp / 16) * 20 + B * 256) * 4; }
+
+template <int W>
+static void launch_mla_attn_w(dim3 grid, size_t lds, hipStream_t s, const uint16_t* qa, const uint16_t* cache, int L,
+                              int R, float sm_scale, int n_splits, float* part) {
+    static std::mutex mu;
+    static size_t granted = 0;  // largest dynamic LDS size set so far
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (lds > granted) {
+            TH_HIP(hipFuncSetAttribute((const void*)mla_attn_kernel<W>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds));
+            granted = lds;
+        }
     }
+    hipLaunchKernelGGL(mla_attn_kernel<W>, grid, dim3(MLA_THREADS), lds, s, qa, cache, L, R, sm_scale, n_splits, part);
+}
+
+template <int... Ks>
+static void launch_mla_attn_any(std::integer_sequence<int, Ks...>, int W, dim3 grid, size_t lds, hipStream_t s,
+                                const uint16_t* qa, const uint16_t* cache, int L, int R, float sm_scale, int n_splits,
+                                float* part) {
+    bool done = false;
+    ((W == 32 * (Ks + 1) ? (launch_mla_attn_w<32 * (Ks + 1)>(grid, lds, s, qa, cache, L, R, sm_scale, n_splits, part),
+                            done = true)
+                         : false),
+     ...);
+    TH_REQUIRE(done, "latent row width must be a multiple of 32 up to 576");
+}
+
+static void launch_mla_attn(size_t W, dim3 grid, size_t lds, hipStream_t s, const uint16_t* qa, const uint16_t* cache,
+                            int L, int R, float sm_scale, int n_splits, float* part) {
+    launch_mla_attn_any(std::make_integer_sequence<int, MLA_WMAX / 32>{}, (int)W, grid, lds, s, qa, cache, L, R,
+                        sm_scale, n_splits, part);
 }
 
 }  // namespace th
@@ -244,7 +429,8 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     TH_API_BEGIN
     TH_REQUIRE(dev && q_nope && q_rope && cache && w_uk && w_uv && out, "null argument");
     TH_REQUIRE(H == MLA_H, "this kernel serves 16 heads");
-    TH_REQUIRE(r % 16 == 0 && r <= 512 && dr % 8 == 0 && (r + dr) % 32 == 0, "latent widths: r <= 512, (r+dr) % 32 == 0");
+    TH_REQUIRE(r % 16 == 0 && r <= 512 && dr % 8 == 0 && (r + dr) % 32 == 0 && r + dr <= MLA_WMAX,
+               "latent widths: r <= 512, r + dr <= 576, (r + dr) % 32 == 0");
     TH_REQUIRE(L > 0 && B > 0 && B <= 16, "1 <= B <= 16 sequences");
     TH_REQUIRE(w_uk->bits == 8 && w_uk->per_row && w_uk->rows == H * r && w_uk->cols == dn, "w_uk must be q8 rowwise [H*r][dn]");
     TH_REQUIRE(w_uv->bits == 8 && w_uv->per_row && w_uv->rows == H * dv && w_uv->cols == r, "w_uv must be q8 rowwise [H*dv][r]");
@@ -257,34 +443,34 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     const size_t W = r + dr;
     const int n_splits = (int)ceil_div(L, (size_t)MLA_SPLIT);
     TH_REQUIRE(n_splits <= 64, "L above 8192 positions");
+    TH_REQUIRE(dn % 4 == 0 && B * w_uk->Kp <= 8192 && B * w_uv->Kp <= 8192,
+               "qk_nope width must be a multiple of 4, and B * width <= 8192 for both projections");
     // workspace: A operand, split records, o_lat
-    const size_t qa_bytes = B * 3 * H * W * 2;
+    const size_t qa_bytes = B * 2 * H * W * 2;
     const size_t part_bytes = B * (size_t)n_splits * H * (r + 2) * 4;
     const size_t olat_bytes = B * H * r * 4;
     char* ws = (char*)device_scratch(dev, round_up(qa_bytes, 256) + round_up(part_bytes, 256) + olat_bytes);
     uint16_t* qa = (uint16_t*)ws;
     float* part = (float*)(ws + round_up(qa_bytes, 256));
     float* olat = (float*)(ws + round_up(qa_bytes, 256) + round_up(part_bytes, 256));
-    int* counters = device_counters(dev, B);
     // 1. absorb
-    hipLaunchKernelGGL(mla_q8_heads_kernel<0>, dim3((unsigned)H, (unsigned)(r / 16)), dim3(256), B * dn * 4, s,
+    hipLaunchKernelGGL(mla_q8_heads_kernel<0>, dim3((unsigned)H, (unsigned)(r / 16)), dim3(256), head_gemv_lds(B, w_uk->Kp), s,
                        (const uint8_t*)w_uk->data, (const float*)w_uk->scales, (int)r, (int)dn, (int)w_uk->Kp, (int)B,
                        (int)H, (const float*)q_nope->ptr, (int)(H * dn), (int)dn, (float*)nullptr, qa,
                        (const float*)q_rope->ptr, (int)dr);
     TH_LAUNCH_CHECK();
     // 2. latent attention
-    const size_t lds = (size_t)MLA_CHUNK * W * 2 + (size_t)MLA_H * MLA_CHUNK * 4 + 4 * MLA_H * 4;
+    const size_t lds = (size_t)MLA_CHUNK * (W + 8) * 2 + (size_t)MLA_WAVES * MLA_H * MLA_CHUNK * 4 +
+                       (size_t)MLA_H * (MLA_CHUNK + 1) * 4;
     TH_REQUIRE(lds <= 150 * 1024, "latent chunk does not fit LDS");
-    static size_t attr_lds = 0;  // largest dynamic LDS size granted so far
-    if (lds > attr_lds) {
-        TH_HIP(hipFuncSetAttribute((const void*)mla_attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        attr_lds = lds;
-    }
-    hipLaunchKernelGGL(mla_attn_kernel, dim3((unsigned)B, (unsigned)n_splits), dim3(256), lds, s, qa,
-                       (const uint16_t*)cache->ptr, (int)L, (int)r, (int)dr, sm_scale, n_splits, part, counters, olat);
+    launch_mla_attn(W, dim3((unsigned)B, (unsigned)n_splits), lds, s, qa, (const uint16_t*)cache->ptr, (int)L, (int)r,
+                    sm_scale, n_splits, part);
+    TH_LAUNCH_CHECK();
+    hipLaunchKernelGGL(mla_merge_kernel, dim3((unsigned)B, (unsigned)H, (unsigned)ceil_div(r, (size_t)128)), dim3(512), 0,
+                       s, part, n_splits, (int)r, olat);
     TH_LAUNCH_CHECK();
     // 3. up-projection
-    hipLaunchKernelGGL(mla_q8_heads_kernel<1>, dim3((unsigned)H, (unsigned)(dv / 16)), dim3(256), B * r * 4, s,
+    hipLaunchKernelGGL(mla_q8_heads_kernel<1>, dim3((unsigned)H, (unsigned)(dv / 16)), dim3(256), head_gemv_lds(B, w_uv->Kp), s,
                        (const uint8_t*)w_uv->data, (const float*)w_uv->scales, (int)dv, (int)r, (int)w_uv->Kp, (int)B,
                        (int)H, olat, (int)(H * r), (int)r, (float*)out->ptr, (uint16_t*)nullptr, (const float*)nullptr,
                        0);

@@ -7,9 +7,11 @@
 //   token's experts in rank order of w * expert(h) + sum of the shared experts.
 //
 // Device flow, no host round trip:
-//   router (one block per token: logits, softmax, top-k)
-//   -> dispatch (one block: per-expert slot lists in token order and work
-//      items of at most 16 rows; shared experts take every token)
+//   router logits (token block x expert block)
+//   -> top-k (one wave per token: softmax, k wave-wide argmaxes)
+//   -> dispatch (one block: per-expert slots in token order and work items
+//      of at most 8 rows for decode-sized batches, else 16; shared experts
+//      take every token)
 //   -> grouped gate/up GEMV (epilogue SwiGLU, bf16 per slot)
 //   -> grouped down GEMV (f32 per slot)
 //   -> combine (per token, rank order, then shared).
@@ -24,96 +26,200 @@
 
 namespace th {
 
-constexpr int MOE_ROWS = 16;  // activation rows per work item (one MFMA row block)
 constexpr int MOE_MAX_K = 16;
+constexpr int MOE_MIN_ROWS = 8;     // rows per work item for decode-sized batches
+constexpr int MOE_SMALL_T = 64;     // batches up to this use MOE_MIN_ROWS, larger ones 16
+constexpr int MOE_MAX_E = 256;      // routed experts (top-k runs in one wave, 4 per lane)
+constexpr int MOE_MAX_NE = 1024;    // routed + shared
+constexpr int ROUTER_TOK = 4;       // tokens per router workgroup
+constexpr int ROUTER_EXP = 16;      // experts per router workgroup (4 per wave)
 
 struct MoeWork { int expert, slot0, rows, pad; };
 
-// One block per token: router logits (f32 dot over d), softmax, top-k.
+// Router logits: workgroup (token block, expert block); wave w takes experts
+// 4w..4w+3 of the block for ROUTER_TOK tokens; lane covers 8 consecutive
+// elements of each 512-element stride of d (f32 products, f32 sums).
 __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restrict__ h, const float* __restrict__ wr,
-                                                         int E, int d, int k, int32_t* __restrict__ topk_idx,
-                                                         float* __restrict__ topk_w) {
-    __shared__ float logit[1024];
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint16_t* hr = h + (size_t)t * d;
-    for (int e = wave; e < E; e += 4) {
-        const float* w = wr + (size_t)e * d;
-        float s = 0.0f;
-        for (int i = lane; i < d; i += 64) s += __uint_as_float((uint32_t)hr[i] << 16) * w[i];
-        s = wave_sum(s);
-        if (lane == 0) logit[e] = s;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        // softmax, cpu.rs:105-124 order: max, exp, sequential sum, scale
-        float mx = -INFINITY;
-        for (int e = 0; e < E; e++) mx = fmaxf(mx, logit[e]);
-        for (int e = 0; e < E; e++) logit[e] = expf(logit[e] - mx);
-        float sum = 0.0f;
-        for (int e = 0; e < E; e++) sum += logit[e];
-        const float inv = 1.0f / sum;
-        for (int e = 0; e < E; e++) logit[e] *= inv;
-        uint32_t used[32] = {0};
-        for (int r = 0; r < k; r++) {
-            int best = -1;
-            float bv = 0.0f;
-            for (int e = 0; e < E; e++) {
-                if (used[e >> 5] >> (e & 31) & 1u) continue;
-                if (best < 0 || logit[e] > bv) { bv = logit[e]; best = e; }
+                                                         int T, int E, int d, float* __restrict__ logits) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * ROUTER_TOK, e0 = blockIdx.y * ROUTER_EXP + wave * 4;
+    float acc[ROUTER_TOK][4];
+#pragma unroll
+    for (int a = 0; a < ROUTER_TOK; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+    for (int k0 = lane * 8; k0 < d; k0 += 512) {
+        float x[ROUTER_TOK][8];
+#pragma unroll
+        for (int a = 0; a < ROUTER_TOK; a++) {
+            const int t = min(t0 + a, T - 1);
+            const uint4 v = *(const uint4*)(h + (size_t)t * d + k0);
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                x[a][2 * j] = __uint_as_float(w4[j] << 16);
+                x[a][2 * j + 1] = __uint_as_float(w4[j] & 0xFFFF0000u);
             }
-            used[best >> 5] |= 1u << (best & 31);
-            topk_idx[(size_t)t * k + r] = best;
+        }
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int e = min(e0 + b, E - 1);
+            const float4 wa = *(const float4*)(wr + (size_t)e * d + k0);
+            const float4 wb = *(const float4*)(wr + (size_t)e * d + k0 + 4);
+            const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+            for (int a = 0; a < ROUTER_TOK; a++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc[a][b] = __builtin_fmaf(x[a][j], w8[j], acc[a][b]);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < ROUTER_TOK; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float v = wave_sum(acc[a][b]);
+            if (lane == 0 && t0 + a < T && e0 + b < E) logits[(size_t)(t0 + a) * E + e0 + b] = v;
+        }
+}
+
+// Softmax over the E logits (max, exp, sum, scale by 1/sum, as cpu.rs:105-124)
+// and top-k by probability, first maximum on ties (sampling.rs:184-194).  One
+// wave per token; lane holds experts lane, lane+64, ...
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                       int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    constexpr int PL = MOE_MAX_E / 64;
+    float p[PL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PL; i++) {
+        const int e = lane + 64 * i;
+        p[i] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
+        mx = fmaxf(mx, p[i]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PL; i++) {
+        p[i] = lane + 64 * i < E ? expf(p[i] - mx) : 0.0f;
+        sum += p[i];
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < PL; i++) p[i] = lane + 64 * i < E ? p[i] * inv : -INFINITY;
+    for (int r = 0; r < k; r++) {
+        // lane's best (lowest index on ties), then the wave's
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < PL; i++)
+            if (p[i] > bv || (p[i] == bv && bi == 0x7fffffff && lane + 64 * i < E)) { bv = p[i]; bi = lane + 64 * i; }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) {
+            topk_idx[(size_t)t * k + r] = bi;
             topk_w[(size_t)t * k + r] = bv;
         }
+#pragma unroll
+        for (int i = 0; i < PL; i++)
+            if (lane + 64 * i == bi) p[i] = -INFINITY;  // taken; -inf never beats a live expert's p >= 0
     }
 }
 
-// Slots: experts 0..E-1 (routed, tokens ascending) then the S shared experts
-// (every token).  offsets[e] = first slot of expert e; token_slot[t*k+r] =
-// slot of the token's rank-r expert; work items cover <= MOE_ROWS slots.
-__global__ __launch_bounds__(256) void moe_dispatch_kernel(const int32_t* __restrict__ topk_idx, int T, int k, int E,
-                                                           int S, int* __restrict__ offsets,
-                                                           int* __restrict__ slot_token, int* __restrict__ token_slot,
-                                                           MoeWork* __restrict__ work, int max_work) {
-    __shared__ int cnt[1024];
-    const int tid = threadIdx.x, NE = E + S;
-    for (int e = tid; e < NE; e += 256) {
+// Slot assignment, deterministic: slots are grouped by expert (routed
+// experts 0..E-1, then the S shared experts with every token) and, within an
+// expert, ordered by entry index t*k + r, i.e. by token.  16 waves each own a
+// contiguous range of entries; a wave's 64 lanes find lanes of the same expert
+// with eight ballots over the expert id bits, so ranks inside a batch come
+// from popcounts, and per-(wave, expert) counts give each wave its first slot.
+// Work items cover at most `rows` slots of one expert.
+__global__ __launch_bounds__(1024) void moe_dispatch_kernel(const int32_t* __restrict__ topk_idx, int T, int k, int E,
+                                                            int S, int rows, int* __restrict__ offsets,
+                                                            int* __restrict__ slot_token, int* __restrict__ token_slot,
+                                                            MoeWork* __restrict__ work, int max_work) {
+    __shared__ int cnt[16][MOE_MAX_E];  // per-wave counts, then per-wave running slots
+    __shared__ int tot[MOE_MAX_NE], base[MOE_MAX_NE + 1], wbase[MOE_MAX_NE + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NE = E + S;
+    const int n = T * k, per = (n + 15) / 16;
+    const int lo = wave * per, hi = min(n, lo + per);
+    for (int i = tid; i < 16 * MOE_MAX_E; i += 1024) (&cnt[0][0])[i] = 0;
+    __syncthreads();
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    auto same_expert = [&](int e, bool live) {
+        uint64_t m = __ballot(live);
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const uint64_t bit = __ballot(live && ((e >> b) & 1));
+            m &= ((e >> b) & 1) ? bit : ~bit;
+        }
+        return m;
+    };
+    for (int i0 = lo; i0 < hi; i0 += 64) {  // pass 1: counts
+        const int i = i0 + lane;
+        const bool live = i < hi;
+        const int e = live ? topk_idx[i] : 0;
+        const uint64_t m = same_expert(e, live);
+        if (live && (m & below) == 0) cnt[wave][e] += __popcll(m);  // the expert's lowest lane
+    }
+    __syncthreads();
+    for (int e = tid; e < NE; e += 1024) {
         int c = 0;
-        if (e < E) {
-            for (int i = 0; i < T * k; i++) c += topk_idx[i] == e;
-        } else {
+        if (e < E)
+            for (int w = 0; w < 16; w++) c += cnt[w][e];
+        else
             c = T;
-        }
-        cnt[e] = c;
+        tot[e] = c;
     }
     __syncthreads();
-    if (tid == 0) {
-        int o = 0;
-        for (int e = 0; e < NE; e++) { offsets[e] = o; o += cnt[e]; }
-        offsets[NE] = o;
+    if (tid == 0) {  // exclusive scans of slots and of work items over experts
+        int o = 0, wo = 0;
+        for (int e = 0; e < NE; e++) {
+            base[e] = o; wbase[e] = wo;
+            o += tot[e]; wo += (tot[e] + rows - 1) / rows;
+        }
+        base[NE] = o; wbase[NE] = wo;
     }
     __syncthreads();
-    for (int e = tid; e < NE; e += 256) {
-        int pos = offsets[e];
-        if (e < E) {
-            for (int i = 0; i < T * k; i++) {
-                if (topk_idx[i] == e) {
-                    slot_token[pos] = i / k;
-                    token_slot[i] = pos;
-                    pos++;
-                }
-            }
-        } else {
-            for (int t = 0; t < T; t++) slot_token[pos + t] = t;
+    for (int e = tid; e <= NE; e += 1024) offsets[e] = base[e];
+    for (int e = tid; e < E; e += 1024) {  // per-wave first slots
+        int o = base[e];
+        for (int w = 0; w < 16; w++) {
+            const int c = cnt[w][e];
+            cnt[w][e] = o;
+            o += c;
         }
     }
-    if (tid == 0) {
-        int w = 0;
-        for (int e = 0; e < NE; e++)
-            for (int m0 = 0; m0 < cnt[e]; m0 += MOE_ROWS)
-                if (w < max_work) work[w++] = MoeWork{e, offsets[e] + m0, min(MOE_ROWS, cnt[e] - m0), 0};
-        for (; w < max_work; w++) work[w] = MoeWork{-1, 0, 0, 0};
+    __syncthreads();
+    for (int i0 = lo; i0 < hi; i0 += 64) {  // pass 2: slots
+        const int i = i0 + lane;
+        const bool live = i < hi;
+        const int e = live ? topk_idx[i] : 0;
+        const uint64_t m = same_expert(e, live);
+        if (live) {
+            const int slot = cnt[wave][e] + __popcll(m & below);
+            token_slot[i] = slot;
+            slot_token[slot] = i / k;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (live && (m & below) == 0) cnt[wave][e] += __popcll(m);
+        __builtin_amdgcn_wave_barrier();
     }
+    for (int s = 0; s < S; s++)
+        for (int t = tid; t < T; t += 1024) slot_token[base[E + s] + t] = t;
+    for (int e = tid; e < NE; e += 1024) {
+        const int c = tot[e];
+        for (int j = 0, w = wbase[e]; j < c; j += rows, w++)
+            if (w < max_work) work[w] = MoeWork{e, base[e] + j, min(rows, c - j), 0};
+    }
+    for (int w = wbase[NE] + tid; w < max_work; w += 1024) work[w] = MoeWork{-1, 0, 0, 0};
 }
 
 // Grouped GEMV source: workgroup -> (work item, tile of that expert's matrix).
@@ -158,16 +264,31 @@ struct EpiMoeStore : EpiNoFinish {
 };
 
 // out[t] = sum_r w[t][r] * y[slot(t, r)] + sum_s y[shared slot]: rank order,
-// then shared experts (f32).
+// then shared experts (f32).  The token's slots and weights are loaded once;
+// each thread covers 4 consecutive outputs.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y, const int* __restrict__ token_slot,
                                                           const float* __restrict__ topk_w, const int* __restrict__ offsets,
                                                           int k, int E, int S, int d, float* __restrict__ out) {
     const int t = blockIdx.x;
-    for (int n = threadIdx.x; n < d; n += 256) {
-        float acc = 0.0f;
-        for (int r = 0; r < k; r++) acc = __builtin_fmaf(topk_w[(size_t)t * k + r], y[(size_t)token_slot[t * k + r] * d + n], acc);
-        for (int s = 0; s < S; s++) acc += y[(size_t)(offsets[E + s] + t) * d + n];
-        out[(size_t)t * d + n] = acc;
+    __shared__ int slot[MOE_MAX_K + 8];
+    __shared__ float wk[MOE_MAX_K];
+    const int tid = threadIdx.x;
+    if (tid < k) { slot[tid] = token_slot[t * k + tid]; wk[tid] = topk_w[(size_t)t * k + tid]; }
+    if (tid >= 64 && tid < 64 + S) slot[MOE_MAX_K + tid - 64] = offsets[E + tid - 64] + t;
+    __syncthreads();
+    for (int n = tid * 4; n < d; n += 1024) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int r = 0; r < k; r++) {
+            const float4 v = *(const float4*)(y + (size_t)slot[r] * d + n);
+            const float w = wk[r];
+            acc.x = __builtin_fmaf(w, v.x, acc.x); acc.y = __builtin_fmaf(w, v.y, acc.y);
+            acc.z = __builtin_fmaf(w, v.z, acc.z); acc.w = __builtin_fmaf(w, v.w, acc.w);
+        }
+        for (int s = 0; s < S; s++) {
+            const float4 v = *(const float4*)(y + (size_t)slot[MOE_MAX_K + s] * d + n);
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+        *(float4*)(out + (size_t)t * d + n) = acc;
     }
 }
 
@@ -189,24 +310,27 @@ struct th_moe {
     MoeWork* work = nullptr;
     uint16_t* hbuf = nullptr;
     float* ybuf = nullptr;
+    float* logits = nullptr;
     bool ready = false;
 };
 
 namespace th {
 
 static void moe_free_work(th_moe* m) {
-    void* ps[] = {m->offsets, m->slot_token, m->token_slot, m->work, m->hbuf, m->ybuf};
+    void* ps[] = {m->offsets, m->slot_token, m->token_slot, m->work, m->hbuf, m->ybuf, m->logits};
     for (void* p : ps)
         if (p) (void)hipFree(p);
     m->offsets = m->slot_token = m->token_slot = nullptr;
     m->work = nullptr;
     m->hbuf = nullptr;
     m->ybuf = nullptr;
+    m->logits = nullptr;
     m->T_cap = 0;
 }
 
-static size_t moe_max_work(const th_moe* m, size_t T) {
-    return ceil_div(T * m->k, MOE_ROWS) + m->E + m->S * ceil_div(T, MOE_ROWS);
+// Work items of `rows` slots: at most one partial item per expert.
+static size_t moe_max_work(const th_moe* m, size_t T, size_t rows) {
+    return ceil_div(T * m->k, rows) + m->E + m->S * ceil_div(T, rows);
 }
 
 static void moe_reserve(th_moe* m, size_t T) {
@@ -217,7 +341,8 @@ static void moe_reserve(th_moe* m, size_t T) {
     TH_HIP(hipMalloc(&m->offsets, (m->E + m->S + 1) * sizeof(int)));
     TH_HIP(hipMalloc(&m->slot_token, slots * sizeof(int)));
     TH_HIP(hipMalloc(&m->token_slot, T * m->k * sizeof(int)));
-    TH_HIP(hipMalloc(&m->work, moe_max_work(m, T) * sizeof(MoeWork)));
+    TH_HIP(hipMalloc(&m->work, moe_max_work(m, T, MOE_MIN_ROWS) * sizeof(MoeWork)));
+    TH_HIP(hipMalloc(&m->logits, T * m->E * sizeof(float)));
     TH_HIP(hipMalloc(&m->hbuf, slots * m->ff * sizeof(uint16_t)));
     TH_HIP(hipMalloc(&m->ybuf, slots * m->d * sizeof(float)));
     m->T_cap = T;
@@ -236,15 +361,18 @@ static void moe_destroy(th_moe* m) {
     delete m;
 }
 
-template <typename Epi, int NW>
+template <int MR, typename Epi, int NW>
 static void moe_grouped_gemv(const th_moe* m, const th_qweight* w0, const uint4* const* data,
                              const _Float16* const* scales, const uint16_t* x, const int* slot_token, size_t max_work,
                              Epi epi) {
     const int tiles = (int)(w0->Np / 16);
     MoeSrc src{m->work, data, scales, slot_token, tiles};
-    const size_t smem = Q4GemvSmem<MOE_ROWS, NW>::bytes((int)(w0->Kp / 128));
+    const size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w0->Kp / 128));
     TH_REQUIRE(smem <= 160 * 1024, "MoE GEMV LDS above 160 KiB");
-    auto k = q4_gemv_kernel<MOE_ROWS, false, true, _Float16, Epi, 2, 2, NW, false, MoeSrc>;
+    // Expert matrices are short (K = 2048 is 16 items of 128), so a
+    // workgroup's life is mostly the latency chain work item -> expert ->
+    // weights; two waves per 8-row tile keep more workgroups resident.
+    auto k = q4_gemv_kernel<MR, false, true, _Float16, Epi, 4, (MR <= 8 ? 4 : 2), NW, false, MoeSrc>;
     static std::mutex mu;
     static size_t done = 0;
     {
@@ -268,7 +396,7 @@ int th_moe_create(th_device* dev, size_t d, size_t ff, size_t E, size_t S, size_
     TH_API_BEGIN
     TH_REQUIRE(dev && out, "null argument");
     TH_REQUIRE(d > 0 && ff > 0 && E > 0 && k > 0 && k <= E && k <= MOE_MAX_K, "bad MoE shape");
-    TH_REQUIRE(E <= 1024 && E + S <= 1024, "at most 1024 experts");
+    TH_REQUIRE(E <= MOE_MAX_E && E + S <= MOE_MAX_NE, "at most 256 routed and 1024 total experts");
     TH_REQUIRE(ff % 8 == 0 && d % 8 == 0, "d and ff must be multiples of 8");
     th_moe* m = new th_moe();
     m->dev = dev; m->d = d; m->ff = ff; m->E = E; m->S = S; m->k = k;
@@ -338,17 +466,29 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
     if (T == 0) return TH_OK;
     moe_reserve(m, T);
     hipStream_t s = m->dev->stream;
-    const size_t max_work = moe_max_work(m, T);
-    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)T), dim3(256), 0, s, (const uint16_t*)h->ptr, m->router,
-                       (int)m->E, (int)m->d, (int)m->k, (int32_t*)topk_idx->ptr, (float*)topk_w->ptr);
+    const int rows = T <= (size_t)MOE_SMALL_T ? MOE_MIN_ROWS : 16;
+    const size_t max_work = moe_max_work(m, T, rows);
+    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)ceil_div(T, ROUTER_TOK), (unsigned)ceil_div(m->E, ROUTER_EXP)),
+                       dim3(256), 0, s, (const uint16_t*)h->ptr, m->router, (int)T, (int)m->E, (int)m->d, m->logits);
     TH_LAUNCH_CHECK();
-    hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(256), 0, s, (const int32_t*)topk_idx->ptr, (int)T, (int)m->k,
-                       (int)m->E, (int)m->S, m->offsets, m->slot_token, m->token_slot, m->work, (int)max_work);
+    hipLaunchKernelGGL(moe_topk_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, s, m->logits, (int)T, (int)m->E,
+                       (int)m->k, (int32_t*)topk_idx->ptr, (float*)topk_w->ptr);
     TH_LAUNCH_CHECK();
-    moe_grouped_gemv<EpiMoeSwiGLU, 4>(m, m->gu[0], m->gu_data, m->gu_scales, (const uint16_t*)h->ptr, m->slot_token,
-                                      max_work, EpiMoeSwiGLU{{}, m->hbuf, (int)m->ff});
-    moe_grouped_gemv<EpiMoeStore, 4>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr, max_work,
-                                     EpiMoeStore{{}, m->ybuf, (int)m->d});
+    hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(1024), 0, s, (const int32_t*)topk_idx->ptr, (int)T, (int)m->k,
+                       (int)m->E, (int)m->S, rows, m->offsets, m->slot_token, m->token_slot, m->work, (int)max_work);
+    TH_LAUNCH_CHECK();
+    const uint16_t* hx = (const uint16_t*)h->ptr;
+    if (rows == MOE_MIN_ROWS) {
+        moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeSwiGLU, 2>(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token,
+                                                        max_work, EpiMoeSwiGLU{{}, m->hbuf, (int)m->ff});
+        moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeStore, 2>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr,
+                                                       max_work, EpiMoeStore{{}, m->ybuf, (int)m->d});
+    } else {
+        moe_grouped_gemv<16, EpiMoeSwiGLU, 4>(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token, max_work,
+                                              EpiMoeSwiGLU{{}, m->hbuf, (int)m->ff});
+        moe_grouped_gemv<16, EpiMoeStore, 4>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr, max_work,
+                                             EpiMoeStore{{}, m->ybuf, (int)m->d});
+    }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, s, m->ybuf, m->token_slot,
                        (const float*)topk_w->ptr, m->offsets, (int)m->k, (int)m->E, (int)m->S, (int)m->d,
                        (float*)out->ptr);

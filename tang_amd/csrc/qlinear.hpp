@@ -226,7 +226,7 @@ struct SingleMatrix {
 
 // Scale access: f16 scales of the items (gq, gq+4) share one 16-byte record,
 // so with four waves per tile one load serves two consecutive items; with
-// eight waves each item loads its own 8-byte half.
+// any other wave count each item loads its own 8-byte half.
 template <typename ST, int NW>
 struct ScaleRec;
 template <>
@@ -239,8 +239,8 @@ struct ScaleRec<_Float16, 4> {
         return (float)__builtin_bit_cast(_Float16, b);
     }
 };
-template <>
-struct ScaleRec<_Float16, 8> {
+template <int NW>
+struct ScaleRec<_Float16, NW> {
     static constexpr int ITEMS = 1;
     typedef uint2 Rec;
     __device__ __forceinline__ static float get(const Rec& v, int, int j) {

@@ -313,7 +313,7 @@ def test_embedding_kat():  # cpu.rs:1000-1016
 
 # ---- MoE and MLA: no reference implementation; pinned by invariants ----------
 
-def _np_dequant_q4(nib, sc, rows, cols):
+def _np_dequant_soa(nib, sc, rows, cols):
     """[rows][cols] f64 from packed nibbles (low nibble = even element) and
     per-group scales: value = (nibble - 8) * scale."""
     b = nib.reshape(rows, -1)
@@ -348,7 +348,7 @@ def test_moe_oracle_matches_dense_mixture(topk):
         mats = []
         for tid, rows, cols in ((4, cfg["ff"], cfg["d"]), (5, cfg["ff"], cfg["d"]), (6, cfg["d"], cfg["ff"])):
             nib, sc16 = capi.synth_q4(capi.synth_seed(5, e, tid), rows, cols)
-            mats.append(_np_dequant_q4(nib, oracle.f16_to_f32(sc16), rows, cols))
+            mats.append(_np_dequant_soa(nib, oracle.f16_to_f32(sc16), rows, cols))
         g = (mats[0] @ x).astype(np.float32).astype(np.float64)
         u = (mats[1] @ x).astype(np.float32).astype(np.float64)
         s = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
