@@ -164,6 +164,133 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
     }
 }
 
+// Decode attention (one query, f16 cache), as attn_split_kernel with a single
+// chunk of SPL positions per workgroup: every K and V row of the split is
+// loaded in one round (raw 16-byte pieces, converted at use), then scores,
+// one softmax pass and P.V; records and the last-arrival merge as above.
+template <int D, int SPL, bool OUT_BF16>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
+                                                          const _Float16* __restrict__ vc, int n_heads, int n_kv_heads,
+                                                          int n_splits, float* __restrict__ part,
+                                                          int* __restrict__ counters, void* __restrict__ out,
+                                                          const int* __restrict__ cache_start_dev) {
+    constexpr int LPK = D / 8;           // lanes per key (eight elements each)
+    constexpr int KPB = 256 / LPK;       // keys per block pass
+    constexpr int KPT = SPL / KPB;       // keys per thread
+    static_assert(KPT >= 1 && KPT * KPB == SPL && LPK <= 64 && 64 % LPK == 0, "bad split shape");
+    __shared__ float red[2][4];
+    __shared__ float vacc[KPB][D + 1];
+    __shared__ int s_last;
+    const int h = blockIdx.x, s = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int slot = tid / LPK, e = tid % LPK;
+    const int kv_dim = n_kv_heads * D;
+    const int kv_h = h / (n_heads / n_kv_heads);
+    const int attend = *cache_start_dev + 1;
+    const int j0 = s * SPL;
+    const int len = max(0, min(SPL, attend - j0));
+    float* recs = part + (size_t)h * n_splits * (D + 2);
+    float* rec = recs + (size_t)s * (D + 2);
+    if (len == 0) {
+        for (int i = tid; i < D + 2; i += 256) st_coherent(&rec[i], i == 0 ? -INFINITY : 0.0f);
+    } else {
+        uint4 kr[KPT], vr[KPT];
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const int row = j0 + min(slot + k * KPB, len - 1);  // clamped: masked below
+            kr[k] = *(const uint4*)(kc + (size_t)row * kv_dim + kv_h * D + e * 8);
+            vr[k] = *(const uint4*)(vc + (size_t)row * kv_dim + kv_h * D + e * 8);
+        }
+        float qv[8];
+        {
+            const float4 a = *(const float4*)(q + (size_t)h * D + e * 8);
+            const float4 b = *(const float4*)(q + (size_t)h * D + e * 8 + 4);
+            qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w; qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+        }
+        const float scale = 1.0f / sqrtf((float)D);
+        float sc[KPT];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const uint32_t w[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                d += qv[2 * i] * (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFF));
+                d += qv[2 * i + 1] * (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+            }
+#pragma unroll
+            for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+            sc[k] = slot + k * KPB < len ? d * scale : -INFINITY;
+            mx = fmaxf(mx, sc[k]);
+        }
+        // block max: the LPK lanes of a key hold equal values
+#pragma unroll
+        for (int o = LPK; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if (lane == 0) red[0][wave] = mx;
+        __syncthreads();
+        const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const float p = expf(sc[k] - M);  // 0 for masked keys
+            lsum += p;
+            const uint32_t w[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc[2 * i] = __builtin_fmaf(p, (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFF)), acc[2 * i]);
+                acc[2 * i + 1] = __builtin_fmaf(p, (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16)), acc[2 * i + 1]);
+            }
+        }
+#pragma unroll
+        for (int o = LPK; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o, 64);
+        if (lane == 0) red[1][wave] = lsum;
+#pragma unroll
+        for (int i = 0; i < 8; i++) vacc[slot][e * 8 + i] = acc[i];
+        __syncthreads();
+        for (int d = tid; d < D; d += 256) {
+            float v = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KPB; k++) v += vacc[k][d];
+            st_coherent(&rec[2 + d], v);
+        }
+        if (tid == 0) {
+            st_coherent(&rec[0], M);
+            st_coherent(&rec[1], (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]));
+        }
+    }
+    if (!last_arrival(&counters[h], n_splits, &s_last)) return;
+    extern __shared__ float recl[];  // [n_splits][D + 2]
+    __shared__ float redm[256];
+    const int total = n_splits * (D + 2);
+#pragma unroll 16
+    for (int i = tid; i < total; i += 256) recl[i] = ld_coherent(&recs[i]);
+    __syncthreads();
+    float mloc = -INFINITY;
+    for (int i = tid; i < n_splits; i += 256) mloc = fmaxf(mloc, recl[(size_t)i * (D + 2)]);
+    const float Mx = block_max_256(mloc, redm);
+    float lloc = 0.0f;
+    __shared__ float wts[256];
+    for (int i = tid; i < n_splits; i += 256) {
+        const float m = recl[(size_t)i * (D + 2)];
+        const float w = m == -INFINITY ? 0.0f : expf(m - Mx);
+        wts[i] = w;
+        lloc += w * recl[(size_t)i * (D + 2) + 1];
+    }
+    const float L = block_sum_256(lloc, redm);  // its barriers also publish wts
+    const float inv = 1.0f / L;
+    for (int d = tid; d < D; d += 256) {
+        float a = 0.0f;
+        for (int i = 0; i < n_splits; i++) a += recl[(size_t)i * (D + 2) + 2 + d] * wts[i];
+        const size_t o = (size_t)h * D + d;
+        if (OUT_BF16) ((uint16_t*)out)[o] = f32_to_bf16_rne(a * inv);
+        else ((float*)out)[o] = a * inv;
+    }
+}
+
 // Dynamic LDS of the split kernel: the merging split stages all records.
 inline size_t attn_merge_lds(int n_splits, int head_dim) { return (size_t)n_splits * (head_dim + 2) * sizeof(float); }
 
@@ -205,6 +332,25 @@ inline void launch_attn_split(const float* q, const void* kc, const void* vc, bo
         case 256: launch_attn_split_d<256, OUT_BF16>(q, kc, vc, f16, cache_start, q_len, n_heads, n_kv_heads, subs, n_splits, part, counters, out, cache_start_dev, s); break;
         default: throw Error(TH_ERR_INVALID, "launch_attn_split: unsupported head_dim");
     }
+}
+
+// Decode attention for the engine: one query, f16 cache, SPL positions per
+// split; counters (n_heads ints) zero on entry and on return.
+template <int SPL, bool OUT_BF16>
+inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float16* vc, int n_heads, int n_kv_heads,
+                               int head_dim, int n_splits, float* part, int* counters, void* out,
+                               const int* cache_start_dev, hipStream_t s) {
+    TH_REQUIRE(n_splits >= 1 && n_splits <= 256, "attention split count out of range");
+    const dim3 grid((unsigned)n_heads, 1, (unsigned)n_splits);
+    const size_t lds = attn_merge_lds(n_splits, head_dim);
+    TH_REQUIRE(lds <= 48 * 1024, "too many attention splits for the LDS merge");
+    switch (head_dim) {
+        case 64: hipLaunchKernelGGL((attn_decode_kernel<64, SPL, OUT_BF16>), grid, dim3(256), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 128: hipLaunchKernelGGL((attn_decode_kernel<128, SPL, OUT_BF16>), grid, dim3(256), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 256: hipLaunchKernelGGL((attn_decode_kernel<256, SPL, OUT_BF16>), grid, dim3(256), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        default: throw Error(TH_ERR_INVALID, "launch_attn_decode: unsupported head_dim");
+    }
+    TH_LAUNCH_CHECK();
 }
 
 void launch_kv_attention(const float* q, const void* kc, const void* vc, bool f16, size_t cache_start, size_t q_len,

@@ -18,6 +18,7 @@
 // The whole step is captured once into a HIP graph that reads the position
 // and token from device memory: one graph launch per token, no host round
 // trip.
+#include <cstdlib>
 #include <vector>
 
 #include "attention.hpp"
@@ -32,7 +33,7 @@ enum : int { T_WQ = 0, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_ATTN_NORM, T_FFN_NO
              T_EMBED = 10, T_FINAL_NORM, T_LM_HEAD, T_KCACHE = 20, T_VCACHE };
 
 constexpr float Q4_SMIN = 0.002f, Q4_SMAX = 0.01f, NORM_STD = 0.02f;
-constexpr int ATTN_SUBS_ENGINE = 2;  // 128 cache positions per attention split
+constexpr int ATTN_SPLIT_ENGINE = 128;  // cache positions per attention workgroup
 
 // state[0] = position, state[1] = current token, state[2] = steps taken
 struct LlamaState { int pos, token, step, pad; };
@@ -260,8 +261,8 @@ static void llama_enqueue_step(th_llama* m) {
         an.ssq = m->ssq; an.nssq = nssq; an.w = m->attn_norm + (size_t)l * d; an.eps = c.eps;
         gemv_engine<true>(m->wqkv[l], m->x, an,
                           EpiQKV{{}, m->q, kc, vc, m->rope_cos, m->rope_sin, m->st, m->qd, m->kvd, hd}, s);
-        launch_attn_split<true>(m->q, kc, vc, true, 0, 1, c.n_heads, c.n_kv_heads, hd, ATTN_SUBS_ENGINE, m->n_splits, m->part,
-                                m->counters, (void*)m->att, (const int*)&m->st->pos, s);
+        launch_attn_decode<ATTN_SPLIT_ENGINE, true>(m->q, kc, vc, c.n_heads, c.n_kv_heads, hd, m->n_splits, m->part,
+                                                    m->counters, (void*)m->att, (const int*)&m->st->pos, s);
         gemv_engine<false>(m->wo[l], m->att, NormArgs{}, EpiAddToSsq{m->x, m->ssq}, s);
         NormArgs fn;
         fn.ssq = m->ssq; fn.nssq = nssq; fn.w = m->ffn_norm + (size_t)l * d; fn.eps = c.eps;
@@ -291,6 +292,25 @@ static void llama_build_graph(th_llama* m) {
     TH_HIP(hipStreamEndCapture(s, &g));
     TH_HIP(hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0));
     TH_HIP(hipGraphDestroy(g));
+}
+
+// One decode step: graph replay, or (TANG_HIP_EAGER=1, for kernel tracers
+// that do not follow graph launches) the same kernels enqueued directly.
+static bool llama_eager() {
+    static const bool eager = [] {
+        const char* e = std::getenv("TANG_HIP_EAGER");
+        return e && e[0] == '1';
+    }();
+    return eager;
+}
+
+static void llama_launch_step(th_llama* m) {
+    if (llama_eager()) {
+        llama_enqueue_step(m);
+        return;
+    }
+    llama_build_graph(m);
+    TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
 }
 
 // Concatenate rows of q4 matrices generated by th_synth_q4 (nib + f16 scales).
@@ -325,7 +345,7 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
     TH_REQUIRE(c.n_heads * c.head_dim == c.d_model, "n_heads*head_dim must equal d_model");
     TH_REQUIRE(c.d_ff % 8 == 0 && c.d_model % 16 == 0, "d_model must be a multiple of 16 and d_ff of 8");
     TH_REQUIRE(c.d_model <= 4096, "the RMSNorm prologue supports d_model <= 4096");
-    TH_REQUIRE(attn_merge_lds((int)ceil_div((size_t)c.max_seq, ATTN_SUB * ATTN_SUBS_ENGINE), c.head_dim) <= 64 * 1024,
+    TH_REQUIRE(attn_merge_lds((int)ceil_div((size_t)c.max_seq, ATTN_SPLIT_ENGINE), c.head_dim) <= 48 * 1024,
                "max_seq too long for the attention merge");
     th_llama* m = new th_llama();
     try {
@@ -334,7 +354,7 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
         m->qd = c.n_heads * c.head_dim;
         m->kvd = c.n_kv_heads * c.head_dim;
         m->max_steps = c.max_seq;
-        m->n_splits = (int)ceil_div((size_t)c.max_seq, ATTN_SUB * ATTN_SUBS_ENGINE);
+        m->n_splits = (int)ceil_div((size_t)c.max_seq, ATTN_SPLIT_ENGINE);
         TH_HIP(hipSetDevice(dev->ordinal));
         const size_t L = c.n_layers, d = c.d_model;
         m->embed = dalloc<uint16_t>((size_t)c.vocab * d);
@@ -490,8 +510,7 @@ int th_llama_step_device(th_llama* m, size_t pos) {
     s.pos = (int)pos;
     s.step = 0;
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
-    llama_build_graph(m);
-    TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+    llama_launch_step(m);
     TH_API_END
 }
 
@@ -505,8 +524,7 @@ int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, in
     LlamaState s{(int)pos, token, 0, 0};
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
-    llama_build_graph(m);
-    for (size_t i = 0; i < n_steps; i++) TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+    for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     if (tokens_out) TH_HIP(hipMemcpy(tokens_out, m->history, n_steps * 4, hipMemcpyDeviceToHost));
     if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
@@ -521,9 +539,9 @@ int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, 
     LlamaState s{(int)pos, token, 0, 0};
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
-    llama_build_graph(m);
+    if (!llama_eager()) llama_build_graph(m);
     TH_HIP(hipEventRecord(m->dev->ev_start, m->dev->stream));
-    for (size_t i = 0; i < n_steps; i++) TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+    for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
     TH_HIP(hipEventRecord(m->dev->ev_stop, m->dev->stream));
     TH_HIP(hipEventSynchronize(m->dev->ev_stop));
     TH_HIP(hipEventElapsedTime(ms, m->dev->ev_start, m->dev->ev_stop));

@@ -335,11 +335,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         return (const typename SR::Rec*)(sc + q4_scale_index(F16S, t, g0, r, 0, GQ));
     };
 
-    // 1. activations for this wave's groups: task (item i, group j, row m)
-    //    covers 32 values (4 chunks); a lane takes up to TPL tasks.
-    constexpr int TPL = MR <= 1 ? 1 : 2;
+    // 1. activations for this wave's groups.  Task (item i, group j, row m)
+    //    covers the 32 values of one group; its four 8-value chunks go to
+    //    four consecutive lanes, so one load instruction reads contiguous
+    //    memory (16 lanes span a 128-value item of one row).  A lane takes
+    //    chunk (task slot) lane + 64 * pass.
+    constexpr int PRE = 2;  // passes loaded before the weight stream
     const int ntask = nmine * 4 * mrows;
-    uint4 xa[TPL][4], xb[TPL][4], nw[TPL][4];
+    const int nchunk = ntask * 4;
+    auto chunk_src = [&](int ci, int& xr, int& k0) {
+        const int task = ci >> 2, c = ci & 3;
+        const int m = task % mrows, ij = task / mrows, i = ij >> 2, j = ij & 3;
+        xr = src.x_row(m);
+        k0 = (4 * (wave + NW * i) + j) * 32 + c * 8;
+    };
+    uint4 xa[PRE], xb[PRE], nw[PRE];
     // RMSNorm partials (at most 256 = 4 per lane): loaded now, summed after
     // the weight stream is issued.
     float ssq_raw[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -351,19 +361,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         }
     }
 #pragma unroll
-    for (int tt = 0; tt < TPL; tt++) {
-        int task = lane + tt * 64;
-        task = task < ntask ? task : 0;
-        const int m = task % mrows, ij = task / mrows, i = ij >> 2, j = ij & 3;
-        const int g = 4 * (wave + NW * i) + j;
-        const int xr = src.x_row(m);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            load_x8<LOADF32, VEC>(xin, xr, ldx, K, g * 32 + c * 8, xa[tt][c], xb[tt][c]);
-            if (NORM) {
-                uint4 dummy;
-                load_x8<false, VEC>(norm.w, 0, 0, K, g * 32 + c * 8, nw[tt][c], dummy);
-            }
+    for (int pp = 0; pp < PRE; pp++) {
+        int ci = lane + pp * 64;
+        ci = ci < nchunk ? ci : 0;
+        int xr, k0;
+        chunk_src(ci, xr, k0);
+        load_x8<LOADF32, VEC>(xin, xr, ldx, K, k0, xa[pp], xb[pp]);
+        if (NORM) {
+            uint4 dummy;
+            load_x8<false, VEC>(norm.w, 0, 0, K, k0, nw[pp], dummy);
         }
     }
     // 2. weights and scales in flight
@@ -381,58 +387,69 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         const float tot = wave_sum_fixed(part);
         inv_rms = 1.0f / sqrtf(tot / (float)K + norm.eps);
     }
-    // 3. stage: bf16 pairs in nibble-pair order; f32 input as hi/lo rows
-    auto stage = [&](int task, const uint4* ra, const uint4* rb, const uint4* rw) {
+    // 3. stage: bf16 pairs in nibble-pair order; f32 input as hi/lo rows.
+    //    The group's bias needs the sum over its four chunks: partial sums
+    //    meet across the four lanes (every lane of a pass takes part, so the
+    //    shuffles see defined values; surplus lanes write nothing).
+    auto stage = [&](int ci, bool live, const uint4& ra, const uint4& rb, const uint4& rw) {
+        const int task = ci >> 2, c = ci & 3;
         const int m = task % mrows, ij = task / mrows;
-        float s_hi = 0.0f, s_lo = 0.0f;
+        float xv[8];
+        if (LOADF32) {
+            xv[0] = __uint_as_float(ra.x); xv[1] = __uint_as_float(ra.y);
+            xv[2] = __uint_as_float(ra.z); xv[3] = __uint_as_float(ra.w);
+            xv[4] = __uint_as_float(rb.x); xv[5] = __uint_as_float(rb.y);
+            xv[6] = __uint_as_float(rb.z); xv[7] = __uint_as_float(rb.w);
+        } else {
+            const uint32_t w4[4] = {ra.x, ra.y, ra.z, ra.w};
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float xv[8];
-            if (LOADF32) {
-                xv[0] = __uint_as_float(ra[c].x); xv[1] = __uint_as_float(ra[c].y);
-                xv[2] = __uint_as_float(ra[c].z); xv[3] = __uint_as_float(ra[c].w);
-                xv[4] = __uint_as_float(rb[c].x); xv[5] = __uint_as_float(rb[c].y);
-                xv[6] = __uint_as_float(rb[c].z); xv[7] = __uint_as_float(rb[c].w);
-            } else {
-                const uint32_t w4[4] = {ra[c].x, ra[c].y, ra[c].z, ra[c].w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
-                    xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
-                }
-            }
-            if (NORM) {
-                const uint32_t w4[4] = {rw[c].x, rw[c].y, rw[c].z, rw[c].w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    // cpu.rs:146: x * inv_rms * w
-                    xv[2 * e] = xv[2 * e] * inv_rms * bf16_bits_to_f32(w4[e] & 0xFFFF);
-                    xv[2 * e + 1] = xv[2 * e + 1] * inv_rms * bf16_bits_to_f32(w4[e] >> 16);
-                }
-            }
-            uint32_t hi[8], lo[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                hi[e] = f32_to_bf16_bits(xv[e]);
-                const float fh = bf16_bits_to_f32(hi[e]);
-                s_hi += fh;
-                if (XF32) {
-                    lo[e] = f32_to_bf16_bits(xv[e] - fh);
-                    s_lo += bf16_bits_to_f32(lo[e]);
-                }
-            }
-            if (XF32) {
-                xw[((size_t)ij * MR + 2 * m) * 4 + c] = pack_x_q4(hi);
-                xw[((size_t)ij * MR + 2 * m + 1) * 4 + c] = pack_x_q4(lo);
-            } else {
-                xw[((size_t)ij * MR + m) * 4 + c] = pack_x_q4(hi);
+            for (int e = 0; e < 4; e++) {
+                xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
+                xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
             }
         }
+        if (NORM) {
+            const uint32_t w4[4] = {rw.x, rw.y, rw.z, rw.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // cpu.rs:146: x * inv_rms * w
+                xv[2 * e] = xv[2 * e] * inv_rms * bf16_bits_to_f32(w4[e] & 0xFFFF);
+                xv[2 * e + 1] = xv[2 * e + 1] * inv_rms * bf16_bits_to_f32(w4[e] >> 16);
+            }
+        }
+        uint32_t hi[8], lo[8];
+        float s_hi = 0.0f, s_lo = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            hi[e] = f32_to_bf16_bits(xv[e]);
+            const float fh = bf16_bits_to_f32(hi[e]);
+            s_hi += fh;
+            if (XF32) {
+                lo[e] = f32_to_bf16_bits(xv[e] - fh);
+                s_lo += bf16_bits_to_f32(lo[e]);
+            }
+        }
+        // group sum over the four chunk lanes: (c0 + c1) + (c2 + c3)
+        s_hi += __shfl_xor(s_hi, 1, 64);
+        s_hi += __shfl_xor(s_hi, 2, 64);
         if (XF32) {
-            bw[ij * BS + 2 * m] = -136.0f * s_hi;
-            bw[ij * BS + 2 * m + 1] = -136.0f * s_lo;
+            s_lo += __shfl_xor(s_lo, 1, 64);
+            s_lo += __shfl_xor(s_lo, 2, 64);
+        }
+        if (!live) return;
+        if (XF32) {
+            xw[((size_t)ij * MR + 2 * m) * 4 + c] = pack_x_q4(hi);
+            xw[((size_t)ij * MR + 2 * m + 1) * 4 + c] = pack_x_q4(lo);
         } else {
-            bw[ij * BS + m] = -136.0f * s_hi;
+            xw[((size_t)ij * MR + m) * 4 + c] = pack_x_q4(hi);
+        }
+        if (c == 0) {
+            if (XF32) {
+                bw[ij * BS + 2 * m] = -136.0f * s_hi;
+                bw[ij * BS + 2 * m + 1] = -136.0f * s_lo;
+            } else {
+                bw[ij * BS + m] = -136.0f * s_hi;
+            }
         }
     };
     if (lane == 0) *zero = make_uint4(0, 0, 0, 0);
@@ -440,24 +457,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     for (int ij = lane; ij < nmine * 4; ij += 64)
         for (int e = mr_live; e < BS; e++) bw[ij * BS + e] = 0.0f;
 #pragma unroll
-    for (int tt = 0; tt < TPL; tt++) {
-        const int task = lane + tt * 64;
-        if (task < ntask) stage(task, xa[tt], xb[tt], nw[tt]);
+    for (int pp = 0; pp < PRE; pp++) {
+        const int ci = lane + pp * 64;
+        if (pp * 64 < nchunk) stage(ci < nchunk ? ci : 0, ci < nchunk, xa[pp], xb[pp], nw[pp]);  // wave-uniform test
     }
-    for (int task = lane + TPL * 64; task < ntask; task += 64) {
-        uint4 ra[4], rb[4], rw[4];
-        const int m = task % mrows, ij = task / mrows, i = ij >> 2, j = ij & 3;
-        const int g = 4 * (wave + NW * i) + j;
-        const int xr = src.x_row(m);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            load_x8<LOADF32, VEC>(xin, xr, ldx, K, g * 32 + c * 8, ra[c], rb[c]);
-            if (NORM) {
-                uint4 dummy;
-                load_x8<false, VEC>(norm.w, 0, 0, K, g * 32 + c * 8, rw[c], dummy);
-            }
+    for (int base = PRE * 64; base < nchunk; base += 64) {  // wave-uniform loop
+        const int ci = base + lane;
+        const int cc = ci < nchunk ? ci : 0;
+        int xr, k0;
+        chunk_src(cc, xr, k0);
+        uint4 ra, rb, rw = make_uint4(0, 0, 0, 0);
+        load_x8<LOADF32, VEC>(xin, xr, ldx, K, k0, ra, rb);
+        if (NORM) {
+            uint4 dummy;
+            load_x8<false, VEC>(norm.w, 0, 0, K, k0, rw, dummy);
         }
-        stage(task, ra, rb, rw);
+        stage(cc, ci < nchunk, ra, rb, rw);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();

@@ -21,7 +21,8 @@ from llama_ref import CONFIG_7B, OracleLlama  # noqa: E402
 # token there depends on summation order).  Token 10 was chosen by scanning
 # first tokens 1..40 on the device for the largest minimum top-2 gap among
 # trajectories that visit more than one token (min gap 9.1e-5, 3 distinct
-# tokens); the gaps of every step are stored with the tokens.
+# tokens); the gaps of every step are stored with the tokens, and so are the
+# five largest logits of every step, for the teacher-forced check.
 SEED, KV_SEED, PREFILL, FIRST_TOKEN, STEPS = 3, 33, 2048, 10, 128
 
 
@@ -33,9 +34,11 @@ def main():
     def progress(i, tok):
         print("step %d token %d (%.1fs)" % (i, tok, time.time() - t0), flush=True)
 
-    toks, margins, logits = ref.generate(FIRST_TOKEN, PREFILL, STEPS, progress=progress)
+    top = []
+    toks, margins, logits = ref.generate(FIRST_TOKEN, PREFILL, STEPS, progress=progress, top=top)
     out = dict(config=CONFIG_7B, seed=SEED, kv_seed=KV_SEED, prefill=PREFILL, first_token=FIRST_TOKEN, steps=STEPS,
                tokens=toks, margins=margins, last_logits_head=[float(v) for v in logits[:512]],
+               top5_ids=[t[0] for t in top], top5_logits=[t[1] for t in top], logit_absmax=[t[2] for t in top],
                generator="th_synth_* (xoshiro256**), oracle or_llama_decode_step")
     with open(os.path.join(HERE, "llama7b_decode.json"), "w") as f:
         json.dump(out, f)

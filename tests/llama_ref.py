@@ -77,7 +77,9 @@ class OracleLlama:
                                                 oracle.p(self.vc), int(token), int(pos), oracle.p(logits), threads)
         return tok, logits
 
-    def generate(self, token, pos, n_steps, threads=0, progress=None):
+    def generate(self, token, pos, n_steps, threads=0, progress=None, top=None):
+        """Greedy steps; with a list `top`, appends each step's five largest
+        logits as (ids, values, max |logit|)."""
         toks, margins = [], []
         logits = None
         for i in range(n_steps):
@@ -85,6 +87,9 @@ class OracleLlama:
             top2 = np.sort(logits)[-2:]
             toks.append(int(token))
             margins.append(float(top2[1] - top2[0]))
+            if top is not None:
+                ids = np.argsort(-logits, kind="stable")[:5]
+                top.append(([int(j) for j in ids], [float(logits[j]) for j in ids], float(np.abs(logits).max())))
             if progress:
                 progress(i, token)
         return toks, margins, logits
