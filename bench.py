@@ -1,6 +1,7 @@
 """Headline benchmark: int4 group-32 GEMV HBM bandwidth (
 11008x4096, M=1, bf16 activations) plus the 7B-shape int4 batch-1 decode rate
-(config 3), on one MI355X.
+(config 3), on one MI355X; also config 1 (int8 GEMV), config 4 (MoE),
+config 5 (MLA) and the prefill GEMM as secondary sections.
 
 One "step" is one GEMV launch over one batch (M=1) of synthetic activations.
 The timed loop cycles through enough distinct weight copies (>256 MiB) that
@@ -38,17 +39,57 @@ CFG7B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=32, head_dim=128,
              max_seq=2176, eps=1e-5, rope_theta=1e4)
 
 
-def gemv_bench(dev, m, steps, warmup):
+def gemv_bench(dev, m, steps, warmup, graph=True):
+    """Elapsed ms of `steps` config-2 linears over N_COPIES weight copies;
+    graph=True replays them as one HIP graph (the decode engine's launch
+    mode), False launches each on the stream."""
     nib, sc16 = capi.synth_q4(2, N, K)
     ws = [dev.q4_upload_packed(nib, sc16, N, K, capi.F16) for _ in range(N_COPIES)]
     x = dev.upload(capi.synth_normal(3, m * K, 1.0, capi.BF16), capi.BF16)
     y = dev.alloc(m * N)
     if warmup:
         dev.bench_linear(x, m, ws, y, warmup)
-    ms = dev.bench_linear(x, m, ws, y, steps)
+    ms = dev.bench_linear(x, m, ws, y, steps, use_graph=graph)
     for w in ws:
         w.free()
     return ms
+
+
+Q8_BYTES = 4096 * 4096 + 3 * 4096 * 4  # config 1: W, row scales, x, y
+
+
+def q8_bench(dev, steps, copies=18):
+    """Config 1: int8 4096x4096 GEMV, per-row scales, f32 x (18 copies =
+    302 MB > MALL), graph-launched."""
+    q, rs = capi.synth_q8_rowwise(1, 4096, 4096)
+    ws = [dev.q8_upload_rowwise(q, rs, 4096, 4096) for _ in range(copies)]
+    x = dev.upload(capi.synth_normal(11, 4096, 1.0, capi.F32))
+    y = dev.alloc(4096)
+    dev.bench_linear(x, 1, ws, y, 48)
+    ms = dev.bench_linear(x, 1, ws, y, steps, use_graph=True)
+    for w in ws:
+        w.free()
+    us = ms * 1e3 / steps
+    return dict(workload="q8 per-row GEMV 4096x4096, M=1, f32 activations (BASELINE config 1)", us=round(us, 3),
+                gbs=round(Q8_BYTES / us / 1e3, 1), frac_hbm=round(Q8_BYTES / us / 1e3 / PEAK_HBM_GBS, 4))
+
+
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def prefill_bench(dev, m, steps=30):
+    """Prefill-shaped int4 GEMM on the config-2 matrix: MFMA path."""
+    nib, sc16 = capi.synth_q4(2, N, K)
+    ws = [dev.q4_upload_packed(nib, sc16, N, K, capi.F16) for _ in range(3)]
+    x = dev.upload(capi.synth_normal(3, m * K, 1.0, capi.BF16), capi.BF16)
+    y = dev.alloc(m * N)
+    dev.bench_linear(x, m, ws, y, 3)
+    ms = dev.bench_linear(x, m, ws, y, steps, use_graph=True)
+    for w in ws:
+        w.free()
+    us = ms * 1e3 / steps
+    tf = 2.0 * m * N * K / us / 1e6
+    return dict(M=m, us=round(us, 1), tflops=round(tf, 1), frac_mfma_bf16=round(tf / PEAK_BF16_TFLOPS, 4))
 
 
 def decode_bytes_per_token(c, t_attended):
@@ -204,12 +245,16 @@ def main():
     ms = gemv_bench(dev, 1, args.steps, args.warmup)
     us = ms * 1e3 / args.steps
     gbs = GEMV_BYTES[1] / us / 1e3
+    ms_stream = gemv_bench(dev, 1, args.steps, 0, graph=False)
+    us_stream = ms_stream * 1e3 / args.steps
     extra = {}
     for m in (4, 8, 16):
         msm = gemv_bench(dev, m, max(args.steps // 4, 48), 24)
         usm = msm * 1e3 / max(args.steps // 4, 48)
         extra["M=%d" % m] = dict(us=round(usm, 3), gbs=round(GEMV_BYTES[m] / usm / 1e3, 1),
                                  frac=round(GEMV_BYTES[m] / usm / 1e3 / PEAK_HBM_GBS, 4))
+    q8 = q8_bench(dev, max(args.steps // 2, 100))
+    prefill = [prefill_bench(dev, m) for m in (512, 2048)]
     decode = None if args.no_decode else decode_bench(dev, args.decode_steps)
     moe = None if args.no_moe_mla else [moe_bench(dev, 16, 200), moe_bench(dev, 512, 50)]
     mla = None if args.no_moe_mla else mla_bench(dev, 400)
@@ -228,12 +273,16 @@ def main():
         "dtype": "int4 weights x bf16 activations, fp32 accumulate",
         "data": "synthetic (seeded xoshiro256**; int4 ~U[-8,7], f16 scales ~U[0.002,0.01], x bf16 ~N(0,1))",
         "config": {"workload": "q4 g32 GEMV 11008x4096, M=1, bf16 activations (BASELINE config 2), "
-                               "%d rotating weight copies (305 MB > 256 MB MALL)" % N_COPIES,
+                               "%d rotating weight copies (305 MB > 256 MB MALL), launches replayed as one HIP graph"
+                               % N_COPIES,
+                   "stream_launched": dict(us=round(us_stream, 3), gbs=round(GEMV_BYTES[1] / us_stream / 1e3, 1)),
                    "M_sweep": extra},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES,
                      "traffic_source": "profiles/q4_gemv_config2.md (FETCH_SIZE/WRITE_SIZE, copy-calibrated)"},
         "cpu_baseline": cpu,
+        "q8_config1": q8,
+        "prefill_gemm_config2_matrix": prefill,
         "decode_7b": decode,
         "moe_config4": moe,
         "mla_config5": mla,

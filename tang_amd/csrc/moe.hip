@@ -369,9 +369,8 @@ static void moe_grouped_gemv(const th_moe* m, const th_qweight* w0, const uint4*
     MoeSrc src{m->work, data, scales, slot_token, tiles};
     const size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w0->Kp / 128));
     TH_REQUIRE(smem <= 160 * 1024, "MoE GEMV LDS above 160 KiB");
-    // Expert matrices are short (K = 2048 is 16 items of 128), so a
-    // workgroup's life is mostly the latency chain work item -> expert ->
-    // weights; two waves per 8-row tile keep more workgroups resident.
+    // Expert matrices are short (K = 2048 is 16 items of 128): every item of
+    // a wave in flight at once.
     auto k = q4_gemv_kernel<MR, false, true, _Float16, Epi, 4, (MR <= 8 ? 4 : 2), NW, false, MoeSrc>;
     static std::mutex mu;
     static size_t done = 0;
@@ -479,9 +478,9 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
     TH_LAUNCH_CHECK();
     const uint16_t* hx = (const uint16_t*)h->ptr;
     if (rows == MOE_MIN_ROWS) {
-        moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeSwiGLU, 2>(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token,
+        moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeSwiGLU, 4>(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token,
                                                         max_work, EpiMoeSwiGLU{{}, m->hbuf, (int)m->ff});
-        moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeStore, 2>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr,
+        moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeStore, 4>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr,
                                                        max_work, EpiMoeStore{{}, m->ybuf, (int)m->d});
     } else {
         moe_grouped_gemv<16, EpiMoeSwiGLU, 4>(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token, max_work,

@@ -26,32 +26,34 @@ static bool x_vec_ok(const void* x, size_t ldx, size_t K) {
     return K % 8 == 0 && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0;
 }
 
-template <int M, bool XF32, typename ST, bool VEC>
-static void q4_gemv_launch_v(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
+template <int M, bool XF32, typename ST, bool VEC, typename Src>
+static void q4_gemv_launch_v(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s,
+                             Src src) {
     constexpr int MR = XF32 ? 2 * M : M;
     EpiStore epi{y, (int)ldy};
-    if (w->Np / 16 < 512) {  // few tiles: split K over eight waves per tile
+    if (M >= 8 || w->Np / 16 < 512) {  // few tiles, or big LDS staging: split K over eight waves per tile
         const size_t smem = Q4GemvSmem<MR, 8>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
-        auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 8>;
+        auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 8, false, Src>;
         set_smem(k, smem);
         hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(512), smem, s, (const uint4*)w->data,
-                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, SingleMatrix{});
+                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, src);
     } else {
         const size_t smem = Q4GemvSmem<MR, 4>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
-        auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 4>;
+        auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 4, false, Src>;
         set_smem(k, smem);
         hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
-                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, SingleMatrix{});
+                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, src);
     }
     TH_LAUNCH_CHECK();
 }
 
-template <int M, bool XF32, typename ST>
-static void q4_gemv_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
-    if (x_vec_ok(x, ldx, w->cols)) q4_gemv_launch_v<M, XF32, ST, true>(w, x, ldx, y, ldy, s);
-    else q4_gemv_launch_v<M, XF32, ST, false>(w, x, ldx, y, ldy, s);
+template <int M, bool XF32, typename ST, typename Src = SingleMatrix>
+static void q4_gemv_launch(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s,
+                           Src src = Src{}) {
+    if (x_vec_ok(x, ldx, w->cols)) q4_gemv_launch_v<M, XF32, ST, true>(w, x, ldx, y, ldy, s, src);
+    else q4_gemv_launch_v<M, XF32, ST, false>(w, x, ldx, y, ldy, s, src);
 }
 
 template <bool XF32, typename ST>
@@ -62,6 +64,14 @@ static void q4_gemv_dispatch(const th_qweight* w, const void* x, size_t m, size_
         case 2: q4_gemv_launch<2, XF32, ST>(w, x, ldx, y, ldy, s); break;
         case 3: q4_gemv_launch<3, XF32, ST>(w, x, ldx, y, ldy, s); break;
         case 4: q4_gemv_launch<4, XF32, ST>(w, x, ldx, y, ldy, s); break;
+        case 5: case 6: case 7: case 8:  // bf16 rows only: an 8-row tile, live rows = m
+            if constexpr (!XF32) {
+                SingleMatrixRows src;
+                src.rows = (int)m;
+                q4_gemv_launch<8, false, ST, SingleMatrixRows>(w, x, ldx, y, ldy, s, src);
+                break;
+            }
+            [[fallthrough]];
         default: throw Error(TH_ERR_INVALID, "q4 gemv: m out of range");
     }
 }
@@ -112,7 +122,8 @@ static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t 
 template <bool XF32, typename ST>
 static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
                         hipStream_t s, th_device* dev) {
-    if (m <= 4) q4_gemv_dispatch<XF32, ST>(w, x, m, ldx, y, ldy, s);
+    const bool tile8_fits = Q4GemvSmem<8, 8>::bytes((int)(w->Kp / 128)) <= 160 * 1024;  // staged rows fit LDS
+    if (m <= 4 || (!XF32 && m <= 8 && tile8_fits)) q4_gemv_dispatch<XF32, ST>(w, x, m, ldx, y, ldy, s);
     else if (m <= 16) q4_mfma_launch<1, 1, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
     else q4_mfma_launch<2, 4, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
 }

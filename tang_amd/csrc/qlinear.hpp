@@ -224,6 +224,19 @@ struct SingleMatrix {
     __device__ __forceinline__ int out_row(int m) const { return m; }
 };
 
+// One matrix with fewer live activation rows than the kernel's tile rows
+// (a run-time row count costs the staging its constant-folded indexing, so
+// only the ragged launches use it).
+struct SingleMatrixRows : SingleMatrix {
+    int rows;
+    template <typename ST>
+    __device__ __forceinline__ bool select(int bid, const uint4*& wt, const ST*& sc, int& t, int& mrows) {
+        t = bid;
+        mrows = rows;
+        return true;
+    }
+};
+
 // Scale access: f16 scales of the items (gq, gq+4) share one 16-byte record,
 // so with four waves per tile one load serves two consecutive items; with
 // any other wave count each item loads its own 8-byte half.
@@ -340,7 +353,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     //    four consecutive lanes, so one load instruction reads contiguous
     //    memory (16 lanes span a 128-value item of one row).  A lane takes
     //    chunk (task slot) lane + 64 * pass.
-    constexpr int PRE = 2;  // passes loaded before the weight stream
+    constexpr int PRE = MR <= 1 ? 2 : (MR <= 4 ? 4 : 8);  // passes loaded before the weight stream
+    constexpr int BATCH = 4;                                // passes per later load round
     const int ntask = nmine * 4 * mrows;
     const int nchunk = ntask * 4;
     auto chunk_src = [&](int ci, int& xr, int& k0) {
@@ -461,18 +475,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         const int ci = lane + pp * 64;
         if (pp * 64 < nchunk) stage(ci < nchunk ? ci : 0, ci < nchunk, xa[pp], xb[pp], nw[pp]);  // wave-uniform test
     }
-    for (int base = PRE * 64; base < nchunk; base += 64) {  // wave-uniform loop
-        const int ci = base + lane;
-        const int cc = ci < nchunk ? ci : 0;
-        int xr, k0;
-        chunk_src(cc, xr, k0);
-        uint4 ra, rb, rw = make_uint4(0, 0, 0, 0);
-        load_x8<LOADF32, VEC>(xin, xr, ldx, K, k0, ra, rb);
-        if (NORM) {
-            uint4 dummy;
-            load_x8<false, VEC>(norm.w, 0, 0, K, k0, rw, dummy);
+    for (int base = PRE * 64; base < nchunk; base += BATCH * 64) {  // wave-uniform loop
+        // every load of the round first, then the staging (one latency per round)
+        uint4 ra[BATCH], rb[BATCH], rw[BATCH];
+#pragma unroll
+        for (int pp = 0; pp < BATCH; pp++) {
+            const int ci = base + pp * 64 + lane;
+            int xr, k0;
+            chunk_src(ci < nchunk ? ci : 0, xr, k0);
+            load_x8<LOADF32, VEC>(xin, xr, ldx, K, k0, ra[pp], rb[pp]);
+            rw[pp] = make_uint4(0, 0, 0, 0);
+            if (NORM) {
+                uint4 dummy;
+                load_x8<false, VEC>(norm.w, 0, 0, K, k0, rw[pp], dummy);
+            }
         }
-        stage(cc, ci < nchunk, ra, rb, rw);
+#pragma unroll
+        for (int pp = 0; pp < BATCH; pp++) {
+            const int ci = base + pp * 64 + lane;
+            if (base + pp * 64 < nchunk) stage(ci < nchunk ? ci : 0, ci < nchunk, ra[pp], rb[pp], rw[pp]);  // wave-uniform
+        }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
