@@ -10,10 +10,11 @@
 //   router logits (token block x expert block)
 //   -> top-k (one wave per token: softmax, k wave-wide argmaxes)
 //   -> dispatch (one block: per-expert slots in token order and work items
-//      of at most 8 rows for decode-sized batches, else 16; shared experts
+//      of at most 8 rows for decode-sized batches, else 64; shared experts
 //      take every token)
-//   -> grouped gate/up GEMV (epilogue SwiGLU, bf16 per slot)
-//   -> grouped down GEMV (f32 per slot)
+//   -> grouped gate/up GEMV (T <= 64) or MFMA GEMM (epilogue SwiGLU, bf16
+//      per slot)
+//   -> grouped down GEMV or MFMA GEMM (f32 per slot)
 //   -> combine (per token, rank order, then shared).
 // Grouped launches size the grid for the worst case; work items past the
 // real ones return at once.
@@ -246,6 +247,58 @@ struct MoeSrc {
     __device__ __forceinline__ int out_row(int m) const { return slot0 + m; }
 };
 
+// Grouped MFMA GEMM source (prefill-sized batches): workgroup row block =
+// one work item of at most 64 slots of one expert.
+struct MoeGemmSrc {
+    static constexpr bool GROUPED = true;
+    const MoeWork* work;
+    const uint4* const* wdata;
+    const _Float16* const* wscales;
+    const int* slot_token;  // null: activation rows are the slots themselves
+    int slot0 = 0;
+    template <typename ST>
+    __device__ __forceinline__ bool select(int by, int, const uint4*& wt, const ST*& sc, int& mrows) {
+        const MoeWork w = work[by];
+        if (w.expert < 0) return false;
+        wt = wdata[w.expert];
+        sc = (const ST*)wscales[w.expert];
+        mrows = w.rows;
+        slot0 = w.slot0;
+        return true;
+    }
+    __device__ __forceinline__ int x_row(int m) const { return slot_token ? slot_token[slot0 + m] : slot0 + m; }
+    __device__ __forceinline__ int out_row(int m) const { return slot0 + m; }
+};
+
+// GEMM epilogues.  D fragment rows n0..n0+3 = 4q..4q+3 of a 16-row tile, so
+// a gate row (tile rows 0..7, lanes q < 2) finds its up row (8 further) in
+// lane + 32.
+struct EpiGemmMoeSwiGLU {
+    uint16_t* hbuf;
+    int ff;
+    __device__ __forceinline__ void operator()(int slot, int n0, int, bool live, const float4_t& v) const {
+        float up[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) up[i] = __shfl_xor(v[i], 32, 64);
+        const int rr = n0 & 15;
+        if (!live || rr >= 8) return;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            hbuf[(size_t)slot * ff + (n0 >> 4) * 8 + rr + i] = f32_to_bf16_rne(swiglu_f64(v[i], up[i]));
+    }
+};
+
+struct EpiGemmMoeStore {
+    float* y;
+    int d;
+    __device__ __forceinline__ void operator()(int slot, int n0, int N, bool live, const float4_t& v) const {
+        if (!live) return;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (n0 + i < N) y[(size_t)slot * d + n0 + i] = v[i];
+    }
+};
+
 // Gate/up tiles hold gate rows 8b..8b+7 then up rows 8b..8b+7 (as in the
 // decode engine): bf16(swiglu(g, u)) per slot.
 struct EpiMoeSwiGLU : EpiNoFinish {
@@ -387,6 +440,22 @@ static void moe_grouped_gemv(const th_moe* m, const th_qweight* w0, const uint4*
     TH_LAUNCH_CHECK();
 }
 
+constexpr int MOE_GEMM_RT = 2;  // 16-row weight tiles per wave
+constexpr int MOE_GEMM_CB = 4;  // 16-slot blocks per work item (64 slots)
+
+template <typename Epi>
+static void moe_grouped_gemm(const th_moe* m, const th_qweight* w0, const uint4* const* data,
+                             const _Float16* const* scales, const uint16_t* x, const int* slot_token, size_t max_work,
+                             Epi epi) {
+    MoeGemmSrc src{m->work, data, scales, slot_token};
+    const unsigned gx = (unsigned)ceil_div(w0->Np / 16, (size_t)(4 * MOE_GEMM_RT));
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<MOE_GEMM_RT, MOE_GEMM_CB, false, _Float16, MoeGemmSrc, Epi>),
+                       dim3(gx, (unsigned)max_work, 1), dim3(256), 0, m->dev->stream, (const uint4*)nullptr,
+                       (const _Float16*)nullptr, (const void*)x, epi, src, (int)w0->rows, (int)w0->cols,
+                       (int)w0->Kp, (int)w0->cols, (int)(w0->Kp / 128));
+    TH_LAUNCH_CHECK();
+}
+
 }  // namespace th
 
 extern "C" {
@@ -465,7 +534,8 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
     if (T == 0) return TH_OK;
     moe_reserve(m, T);
     hipStream_t s = m->dev->stream;
-    const int rows = T <= (size_t)MOE_SMALL_T ? MOE_MIN_ROWS : 16;
+    const bool gemm = T > (size_t)MOE_SMALL_T;  // prefill-sized: grouped MFMA GEMM, 64-slot work items
+    const int rows = gemm ? MOE_GEMM_CB * 16 : MOE_MIN_ROWS;
     const size_t max_work = moe_max_work(m, T, rows);
     hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)ceil_div(T, ROUTER_TOK), (unsigned)ceil_div(m->E, ROUTER_EXP)),
                        dim3(256), 0, s, (const uint16_t*)h->ptr, m->router, (int)T, (int)m->E, (int)m->d, m->logits);
@@ -483,10 +553,10 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
         moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeStore, 4>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr,
                                                        max_work, EpiMoeStore{{}, m->ybuf, (int)m->d});
     } else {
-        moe_grouped_gemv<16, EpiMoeSwiGLU, 4>(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token, max_work,
-                                              EpiMoeSwiGLU{{}, m->hbuf, (int)m->ff});
-        moe_grouped_gemv<16, EpiMoeStore, 4>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr, max_work,
-                                             EpiMoeStore{{}, m->ybuf, (int)m->d});
+        moe_grouped_gemm(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token, max_work,
+                         EpiGemmMoeSwiGLU{m->hbuf, (int)m->ff});
+        moe_grouped_gemm(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr, max_work,
+                         EpiGemmMoeStore{m->ybuf, (int)m->d});
     }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, s, m->ybuf, m->token_slot,
                        (const float*)topk_w->ptr, m->offsets, (int)m->k, (int)m->E, (int)m->S, (int)m->d,

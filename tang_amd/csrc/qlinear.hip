@@ -106,9 +106,12 @@ static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t 
         out = (float*)device_scratch(dev, ks * m * w->rows * sizeof(float));
         ldo = (int)w->rows;
     }
+    GemmDense src;
+    src.M = (int)m;
+    EpiGemmStore epi{out, ldo, (size_t)m * (size_t)ldo};
     hipLaunchKernelGGL((q4_gemm_mfma_kernel<RT, CB, XF32, ST>), dim3(gx, gy, (unsigned)ks), dim3(256), 0, s,
-                       (const uint4*)w->data, (const ST*)w->scales, x, out, (int)m, (int)w->rows,
-                       (int)w->cols, (int)w->Kp, (int)ldx, ldo, gps);
+                       (const uint4*)w->data, (const ST*)w->scales, x, epi, src, (int)w->rows, (int)w->cols,
+                       (int)w->Kp, (int)ldx, gps);
     TH_LAUNCH_CHECK();
     if (ks > 1) {
         const size_t total = m * w->rows;

@@ -763,20 +763,59 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
-template <int RT, int CB, bool XF32, typename ST>
+// Sources of the MFMA GEMM: which weights a workgroup multiplies and which
+// activation rows it takes.  Rows are local to the workgroup's block of
+// CB*16 rows (0 <= m < mrows).
+struct GemmDense {
+    static constexpr bool GROUPED = false;
+    int M;
+    template <typename ST>
+    __device__ __forceinline__ bool select(int by, int rows_per_block, const uint4*& wt, const ST*& sc, int& mrows) {
+        m0 = by * rows_per_block;
+        mrows = min(rows_per_block, M - m0);
+        return true;
+    }
+    int m0 = 0;
+    __device__ __forceinline__ int x_row(int m) const { return m0 + m; }
+    __device__ __forceinline__ int out_row(int m) const { return m0 + m; }
+};
+
+// Epilogue of the MFMA GEMM: D fragment (weight rows n0..n0+3, activation
+// row m) of one lane; `live` is false for rows past the block or the matrix.
+// Called by every lane (pairing epilogues shuffle).
+struct EpiGemmStore {
+    float* y;
+    int ldy;
+    size_t split_stride;  // split-K partials: y + blockIdx.z * split_stride
+    __device__ __forceinline__ void operator()(int out_row, int n0, int N, bool live, const float4_t& v) const {
+        if (!live) return;
+        float* yb = y + (size_t)blockIdx.z * split_stride + (size_t)out_row * ldy;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (n0 + i < N) yb[n0 + i] = v[i];
+    }
+};
+
+template <int RT, int CB, bool XF32, typename ST, typename Src = GemmDense, typename Epi = EpiGemmStore>
 __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restrict__ wt,
                                                            const ST* __restrict__ sc,
-                                                           const void* __restrict__ xin, float* __restrict__ y,
-                                                           int M, int N, int K, int Kp, int ldx, int ldy,
-                                                           int gq_per_split) {
+                                                           const void* __restrict__ xin, Epi epi, Src src,
+                                                           int N, int K, int Kp, int ldx, int gq_per_split) {
     // LDS B tile: [CB][4 j][4 q][16 col] uint4 (8 f16 each)
     __shared__ uint4 bt[CB * 4 * 4 * 16];
+    int mrows = 0;
+    {
+        const uint4* wsel = wt;
+        const ST* ssel = sc;
+        if (!src.select((int)blockIdx.y, CB * 16, wsel, ssel, mrows)) return;
+        wt = wsel;
+        sc = ssel;
+    }
     const int GQ = Kp >> 7;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
     const int tile0 = (blockIdx.x * 4 + wave) * RT;  // first 16-row tile of this wave
     const int NT = (N + 15) >> 4;
-    const int m0 = blockIdx.y * CB * 16;
     const int gq0 = blockIdx.z * gq_per_split;
     const int gq1 = min(GQ, gq0 + gq_per_split);
 
@@ -796,12 +835,13 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
             const int qq = (idx >> 4) & 3;
             const int j = (idx >> 6) & 3;
             const int cb = idx >> 8;
-            const int m = m0 + cb * 16 + col;
+            const int ml = cb * 16 + col;
             const int k0 = gq * 128 + j * 32 + qq * 8;
             float xv[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) xv[e] = 0.0f;
-            if (m < M) {
+            if (ml < mrows) {
+                const int m = src.x_row(ml);
                 if (XF32) {
                     const float* xr = (const float*)xin + (size_t)m * ldx;
                     if (vec && k0 + 8 <= K) {
@@ -891,18 +931,14 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     }
 
     // D layout: lane holds rows 4*(lane/16)+i (weight rows) of column lane%16.
-    float* yb = y + (size_t)blockIdx.z * M * ldy;
 #pragma unroll
     for (int a = 0; a < RT; a++) {
         const int n0 = (tile0 + a) * 16 + 4 * q;
 #pragma unroll
         for (int b = 0; b < CB; b++) {
-            const int m = m0 + b * 16 + r;
-            if (m < M && tile0 + a < NT) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (n0 + i < N) yb[(size_t)m * ldy + n0 + i] = acc[a][b][i];
-            }
+            const int ml = b * 16 + r;
+            const bool live = ml < mrows && tile0 + a < NT;
+            epi(src.out_row(live ? ml : 0), n0, N, live, acc[a][b]);
         }
     }
 }
