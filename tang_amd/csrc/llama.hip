@@ -182,7 +182,13 @@ static void gemv_engine(const th_qweight* w, const void* x, NormArgs norm, Epi e
     TH_REQUIRE(w->bits == 4 && w->scale_dtype == TH_F16, "engine weights must be q4 with f16 scales");
     TH_REQUIRE(!NORM || (w->cols % 16 == 0 && w->cols / 16 <= 256), "RMSNorm prologue supports K <= 4096");
     const bool small = w->Np / 16 < 512;
-    if (small) {
+    if (small && w->Kp / 128 >= 64) {  // few tiles, long K (down projection): sixteen waves per tile
+        const size_t smem = Q4GemvSmem<1, 16>::bytes((int)(w->Kp / 128));
+        TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
+        hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 16, NORM>), dim3((unsigned)(w->Np / 16)),
+                           dim3(1024), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
+                           (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm, SingleMatrix{});
+    } else if (small) {
         const size_t smem = Q4GemvSmem<1, 8>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
         hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 8, NORM>), dim3((unsigned)(w->Np / 16)),

@@ -31,7 +31,14 @@ static void q4_gemv_launch_v(const th_qweight* w, const void* x, size_t ldx, flo
                              Src src) {
     constexpr int MR = XF32 ? 2 * M : M;
     EpiStore epi{y, (int)ldy};
-    if (M >= 8 || w->Np / 16 < 512) {  // few tiles, or big LDS staging: split K over eight waves per tile
+    if (M == 1 && w->Np / 16 < 512 && w->Kp / 128 >= 64) {  // few tiles, long K: sixteen waves per tile
+        const size_t smem = Q4GemvSmem<MR, 16>::bytes((int)(w->Kp / 128));
+        TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
+        auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 16, false, Src>;
+        set_smem(k, smem);
+        hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(1024), smem, s, (const uint4*)w->data,
+                           (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, src);
+    } else if (M >= 8 || w->Np / 16 < 512) {  // few tiles, or big LDS staging: split K over eight waves per tile
         const size_t smem = Q4GemvSmem<MR, 8>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
         auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 8, false, Src>;
