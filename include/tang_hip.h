@@ -203,6 +203,33 @@ int th_llama_set_token(th_llama* m, int32_t token);
  * on the device stream around the step launches. */
 int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, float* ms);
 
+/* ---- sampling (host, crates/tang-infer/src/sampling.rs) ------------------ */
+/* SamplingConfig (sampling.rs:6-20); stop_token < 0 means None. */
+typedef struct {
+    double temperature;        /* 0 = greedy */
+    size_t top_k;              /* 0 = off */
+    double top_p;              /* 1 = off */
+    double repetition_penalty; /* 1 = off */
+    int64_t stop_token;        /* < 0: none */
+    size_t max_tokens;
+} th_sampling_config;
+typedef struct th_sampler th_sampler;
+/* Sampler::with_seed (sampling.rs:67-72). */
+int th_sampler_create(const th_sampling_config* cfg, uint64_t seed, th_sampler** out);
+int th_sampler_destroy(th_sampler* s);
+/* Sampler::sample (sampling.rs:86-160) on host f32 logits [vocab]; past =
+ * tokens seen so far (for the repetition penalty). */
+int th_sampler_sample(th_sampler* s, const float* logits, size_t vocab, const int32_t* past, size_t n_past,
+                      int32_t* token);
+/* generate() (sampling.rs:229-256) on the decode engine: prompt_last is fed
+ * at position pos (positions < pos already in the KV cache); each step runs on
+ * the device, the logits come to the host and the sampler picks the next
+ * token (past = prompt tokens, then the generated ones).  Stops after
+ * cfg.max_tokens or before appending stop_token.  tokens_out receives the
+ * generated tokens (up to max_tokens), *n_out their count. */
+int th_llama_generate_sampled(th_llama* m, th_sampler* s, const int32_t* prompt, size_t n_prompt, size_t pos,
+                              int32_t* tokens_out, size_t* n_out);
+
 /* ---- MoE (DeepSeek-style; no reference implementation) ------------------ */
 typedef struct th_moe th_moe;
 int th_moe_create(th_device* dev, size_t d_model, size_t d_ff, size_t n_experts, size_t n_shared,

@@ -65,6 +65,7 @@ _SIG = {
     "or_argmax_f32": ([_P, _S], _S),
     "or_llama_decode_step": ([_P, _P, _P, _P, _I, _I, _P, _I], _I),
     "or_moe_forward": ([_P, _S, _S, _S, _S, _S, _S, _P, _P, _P, _P, _P, _P, _I], None),
+    "or_sample": ([_P, _P, _P, _S, _P, _S], _S),
     "or_mla_decode": ([_P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _P, _P, _D, _P, _I], None),
 }
 
@@ -275,3 +276,26 @@ def mla_decode(q_nope, q_rope, cache_bf16, B, H, L, dn, dr, r, dv, wuk, wuk_scal
     lib().or_mla_decode(p(q_nope), p(q_rope), p(cache_bf16), B, H, L, dn, dr, r, dv, p(wuk), p(wuk_scale), p(wuv),
                         p(wuv_scale), float(sm_scale), p(out), threads)
     return out
+
+
+class SamplingCfg(ctypes.Structure):
+    """or_sampling_cfg (sampling.rs:6-20); stop_token < 0 means None."""
+    _fields_ = [("temperature", ctypes.c_double), ("top_p", ctypes.c_double),
+                ("repetition_penalty", ctypes.c_double), ("top_k", ctypes.c_size_t),
+                ("max_tokens", ctypes.c_size_t), ("stop_token", ctypes.c_int64)]
+
+
+class OracleSampler:
+    """Restated Sampler (sampling.rs:56-160): config, LCG state, sample()."""
+
+    def __init__(self, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0, seed=42, stop_token=None,
+                 max_tokens=256):
+        self.cfg = SamplingCfg(temperature, top_p, repetition_penalty, top_k, max_tokens,
+                               -1 if stop_token is None else stop_token)
+        self.state = ctypes.c_uint64(seed)
+
+    def sample(self, logits, past=()):
+        lg = np.ascontiguousarray(logits, np.float32)
+        pa = np.ascontiguousarray(past, np.int32)
+        return int(lib().or_sample(ctypes.byref(self.cfg), ctypes.byref(self.state), p(lg), lg.size,
+                                   p(pa) if pa.size else None, pa.size))

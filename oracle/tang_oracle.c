@@ -656,3 +656,117 @@ void or_mla_decode(const float* q_nope, const float* q_rope, const uint16_t* cac
         }
     }
 }
+
+/* ---------------------------------------------------------------------- */
+/* Sampling (crates/tang-infer/src/sampling.rs)                            */
+/* ---------------------------------------------------------------------- */
+
+/* sampling.rs:6-20 SamplingConfig; stop_token < 0 means None. */
+typedef struct {
+    double temperature, top_p, repetition_penalty;
+    size_t top_k, max_tokens;
+    int64_t stop_token;
+} or_sampling_cfg;
+
+/* sampling.rs:77-80: LCG step, 53 high bits as [0, 1). */
+static double or_rand_f64(uint64_t* state) {
+    *state = *state * 6364136223846793005ULL + 1442695040888963407ULL;
+    return (double)(*state >> 11) / (double)(1ULL << 53);
+}
+
+/* sampling.rs:184-194: first index with a strictly greater value. */
+static size_t or_argmax_f64(const double* v, size_t n) {
+    size_t best = 0;
+    double bv = -INFINITY;
+    for (size_t i = 0; i < n; i++)
+        if (v[i] > bv) { bv = v[i]; best = i; }
+    return best;
+}
+
+/* Stable descending order of indices by value (Rust's sort_by is a stable
+ * merge sort; partial_cmp of NaN is treated as Equal).  Insertion-based merge
+ * sort on index arrays. */
+static void or_sort_desc_stable(const double* v, size_t* idx, size_t* tmp, size_t n) {
+    for (size_t w = 1; w < n; w *= 2) {
+        for (size_t lo = 0; lo < n; lo += 2 * w) {
+            size_t mid = lo + w < n ? lo + w : n, hi = lo + 2 * w < n ? lo + 2 * w : n;
+            size_t a = lo, b = mid, o = lo;
+            while (a < mid && b < hi) {
+                /* take from the right run only when it is strictly greater */
+                if (v[idx[b]] > v[idx[a]]) tmp[o++] = idx[b++];
+                else tmp[o++] = idx[a++];
+            }
+            while (a < mid) tmp[o++] = idx[a++];
+            while (b < hi) tmp[o++] = idx[b++];
+        }
+        memcpy(idx, tmp, n * sizeof(size_t));
+    }
+}
+
+/* sampling.rs:86-160 Sampler::sample, including kth_largest (:172-178) and
+ * top_p_filter (:197-215), categorical_sample (:163-175).  logits: n values
+ * (the Scalar -> f64 conversion of :91 is exact from f32). */
+size_t or_sample(const or_sampling_cfg* c, uint64_t* state, const float* logits, size_t n, const int32_t* past,
+                 size_t n_past) {
+    double* p = malloc(n * sizeof(double));
+    size_t* idx = malloc(n * sizeof(size_t));
+    size_t* tmp = malloc(n * sizeof(size_t));
+    size_t result;
+    for (size_t i = 0; i < n; i++) p[i] = (double)logits[i];
+    if (c->repetition_penalty != 1.0) {
+        for (size_t j = 0; j < n_past; j++) {
+            size_t t = (size_t)past[j];
+            if (t < n) {
+                if (p[t] > 0.0) p[t] /= c->repetition_penalty;
+                else p[t] *= c->repetition_penalty;
+            }
+        }
+    }
+    if (c->temperature == 0.0) { result = or_argmax_f64(p, n); goto done; }
+    if (c->temperature != 1.0) {
+        double inv_t = 1.0 / c->temperature;
+        for (size_t i = 0; i < n; i++) p[i] *= inv_t;
+    }
+    {
+        double mx = -INFINITY;
+        for (size_t i = 0; i < n; i++) mx = fmax(mx, p[i]);
+        for (size_t i = 0; i < n; i++) p[i] = exp(p[i] - mx);
+    }
+    if (c->top_k > 0 && c->top_k < n) {
+        for (size_t i = 0; i < n; i++) idx[i] = i;
+        or_sort_desc_stable(p, idx, tmp, n);
+        double thr = p[idx[c->top_k - 1]];
+        for (size_t i = 0; i < n; i++) if (p[i] < thr) p[i] = 0.0;
+    }
+    {
+        double sum = 0.0;
+        for (size_t i = 0; i < n; i++) sum += p[i];
+        if (sum <= 0.0) { result = or_argmax_f64(p, n); goto done; }
+        for (size_t i = 0; i < n; i++) p[i] /= sum;
+    }
+    if (c->top_p < 1.0) {
+        for (size_t i = 0; i < n; i++) idx[i] = i;
+        or_sort_desc_stable(p, idx, tmp, n);
+        double cum = 0.0;
+        size_t cutoff = n;
+        for (size_t r = 0; r < n; r++) {
+            cum += p[idx[r]];
+            if (cum >= c->top_p) { cutoff = r + 1; break; }
+        }
+        for (size_t r = cutoff; r < n; r++) p[idx[r]] = 0.0;
+        double sum = 0.0;
+        for (size_t i = 0; i < n; i++) sum += p[i];
+        if (sum > 0.0) for (size_t i = 0; i < n; i++) p[i] /= sum;
+    }
+    {
+        double r = or_rand_f64(state), cum = 0.0;
+        result = n - 1;
+        for (size_t i = 0; i < n; i++) {
+            cum += p[i];
+            if (r < cum) { result = i; break; }
+        }
+    }
+done:
+    free(p); free(idx); free(tmp);
+    return result;
+}

@@ -92,6 +92,10 @@ SIGNATURES = {
     "th_moe_destroy": ([_P], _I),
     "th_moe_init_synthetic": ([_P, _U64], _I),
     "th_moe_forward": ([_P, _P, _S, _P, _P, _P], _I),
+    "th_sampler_create": ([_P, _U64, _P], _I),
+    "th_sampler_destroy": ([_P], _I),
+    "th_sampler_sample": ([_P, _P, _S, _P, _S, _P], _I),
+    "th_llama_generate_sampled": ([_P, _P, _P, _S, _S, _P, _P], _I),
     "th_mla_decode": ([_P, _P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _F, _P], _I),
     "th_synth_seed": ([_U64, _U64, _U64], _U64),
     "th_synth_q4": ([_U64, _S, _S, _F, _F, _P, _P], _I),
@@ -226,6 +230,47 @@ class QWeight:
         try:
             if self.handle and _lib is not None:
                 _lib.th_qweight_free(self.handle)
+        except Exception:
+            pass
+
+
+class SamplingConfig(ctypes.Structure):
+    """th_sampling_config = SamplingConfig (sampling.rs:6-20); stop_token < 0: None."""
+    _fields_ = [("temperature", ctypes.c_double), ("top_k", ctypes.c_size_t), ("top_p", ctypes.c_double),
+                ("repetition_penalty", ctypes.c_double), ("stop_token", ctypes.c_int64),
+                ("max_tokens", ctypes.c_size_t)]
+
+    def __init__(self, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0, stop_token=None,
+                 max_tokens=256):
+        super().__init__(temperature, top_k, top_p, repetition_penalty, -1 if stop_token is None else stop_token,
+                         max_tokens)
+
+
+class Sampler:
+    """Sampler::with_seed + Sampler::sample (sampling.rs:67-160) through the C ABI."""
+
+    def __init__(self, cfg, seed=42):
+        self.cfg = cfg
+        h = ctypes.c_void_p()
+        check(lib().th_sampler_create(ctypes.byref(cfg), seed, ctypes.byref(h)))
+        self.handle = h
+
+    def sample(self, logits, past=()):
+        lg = np.ascontiguousarray(logits, np.float32)
+        pa = np.ascontiguousarray(past, np.int32)
+        tok = ctypes.c_int32()
+        check(lib().th_sampler_sample(self.handle, ptr(lg), lg.size, ptr(pa) if pa.size else None, pa.size,
+                                      ctypes.byref(tok)))
+        return tok.value
+
+    def close(self):
+        if self.handle:
+            lib().th_sampler_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 

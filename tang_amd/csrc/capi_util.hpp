@@ -31,6 +31,8 @@ inline void check_status(int rc) {
 
 // Grow-only stream-ordered workspace owned by the device.
 void* device_scratch(th_device* dev, size_t bytes);
+// The configuration a sampler was created with (sampling.cpp).
+const th_sampling_config& sampler_config(const th_sampler* s);
 // Zero-initialised ints that kernels leave zero again on exit (arrival
 // counters of the last-workgroup merges); grow-only.
 int* device_counters(th_device* dev, size_t n);

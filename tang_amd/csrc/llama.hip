@@ -33,7 +33,7 @@ enum : int { T_WQ = 0, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_ATTN_NORM, T_FFN_NO
              T_EMBED = 10, T_FINAL_NORM, T_LM_HEAD, T_KCACHE = 20, T_VCACHE };
 
 constexpr float Q4_SMIN = 0.002f, Q4_SMAX = 0.01f, NORM_STD = 0.02f;
-constexpr int ATTN_SPLIT_ENGINE = 128;  // cache positions per attention workgroup
+constexpr int ATTN_SPLIT_ENGINE = 256;  // cache positions per attention workgroup
 
 // state[0] = position, state[1] = current token, state[2] = steps taken
 struct LlamaState { int pos, token, step, pad; };
@@ -487,6 +487,7 @@ int th_llama_fill_kv_synthetic(th_llama* m, size_t len, uint64_t seed) {
         th_synth_normal(th_synth_seed(seed, l, T_KCACHE), n, 1.0f, TH_F16, k[l].data());
         th_synth_normal(th_synth_seed(seed, l, T_VCACHE), n, 1.0f, TH_F16, v[l].data());
     }
+    TH_HIP(hipStreamSynchronize(m->dev->stream));  // the engine stream is non-blocking: drain it first
     for (size_t l = 0; l < L; l++) {
         TH_HIP(hipMemcpy(m->kcache + l * layer, k[l].data(), n * 2, hipMemcpyHostToDevice));
         TH_HIP(hipMemcpy(m->vcache + l * layer, v[l].data(), n * 2, hipMemcpyHostToDevice));
@@ -534,6 +535,37 @@ int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, in
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     if (tokens_out) TH_HIP(hipMemcpy(tokens_out, m->history, n_steps * 4, hipMemcpyDeviceToHost));
     if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
+    TH_API_END
+}
+
+int th_llama_generate_sampled(th_llama* m, th_sampler* smp, const int32_t* prompt, size_t n_prompt, size_t pos,
+                              int32_t* tokens_out, size_t* n_out) {
+    TH_API_BEGIN
+    TH_REQUIRE(m && m->weights_ready, "model not initialised");
+    TH_REQUIRE(smp && prompt && n_prompt > 0 && tokens_out && n_out, "null argument");
+    const th_sampling_config& c = sampler_config(smp);
+    TH_REQUIRE(pos + c.max_tokens <= (size_t)m->cfg.max_seq, "generation runs past max_seq");
+    TH_REQUIRE(c.max_tokens <= (size_t)m->max_steps, "too many steps");
+    for (size_t i = 0; i < n_prompt; i++) TH_REQUIRE(prompt[i] >= 0 && prompt[i] < m->cfg.vocab, "token out of range");
+    *n_out = 0;
+    std::vector<int32_t> past(prompt, prompt + n_prompt);  // generate() passes every token so far
+    std::vector<float> logits((size_t)m->cfg.vocab);
+    LlamaState st{(int)pos, prompt[n_prompt - 1], 0, 0};
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    TH_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
+    hipStream_t s = m->dev->stream;  // non-blocking: every copy goes on it and is waited for
+    for (size_t i = 0; i < c.max_tokens; i++) {
+        llama_launch_step(m);  // advances the device position; its greedy token is replaced below
+        TH_HIP(hipMemcpyAsync(logits.data(), m->logits, logits.size() * 4, hipMemcpyDeviceToHost, s));
+        TH_HIP(hipStreamSynchronize(s));
+        int32_t next = 0;
+        check_status(th_sampler_sample(smp, logits.data(), logits.size(), past.data(), past.size(), &next));
+        if (c.stop_token >= 0 && next == c.stop_token) break;  // sampling.rs:246-250
+        past.push_back(next);
+        tokens_out[(*n_out)++] = next;
+        TH_HIP(hipMemcpyAsync(&m->st->token, &next, sizeof next, hipMemcpyHostToDevice, s));
+        TH_HIP(hipStreamSynchronize(s));
+    }
     TH_API_END
 }
 

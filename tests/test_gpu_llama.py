@@ -5,12 +5,14 @@ Small config: compared live with the oracle (GQA, head_dim 64).
 with tests/golden/llama7b_decode.json, which tests/golden/make_decode_golden.py
 wrote by running the oracle on the same seeded synthetic model.
 """
+import ctypes
 import json
 import os
 
 import numpy as np
 import pytest
 
+import oracle
 from conftest import max_abs_rel
 from llama_ref import CONFIG_7B, CONFIG_SMALL, OracleLlama, device_generate, device_llama
 from tang_amd import capi
@@ -132,3 +134,62 @@ def test_7b_decode_teacher_forced_128_steps(dev):
     finally:
         capi.lib().th_llama_destroy(m)
     print("steps with the oracle's exact token: %d / %d" % (exact, g["steps"]))
+
+
+def _device_steps_oracle_sampler(dev, cfg, prompt, prefill, steps, seed, stop=None, **kw):
+    """generate() (sampling.rs:229-256) composed in Python: one device step
+    at a time (th_llama_generate, 1 step, logits returned) and the oracle
+    sampler on the device's own logits."""
+    s = oracle.OracleSampler(seed=seed, stop_token=stop, **kw)
+    m = device_llama(dev, cfg, 7, 8, prefill)
+    past, out, tok = list(prompt), [], prompt[-1]
+    try:
+        for i in range(steps):
+            _, logits = device_generate(m, cfg, tok, prefill + i, 1)
+            nxt = s.sample(logits, past)
+            if stop is not None and nxt == stop:
+                break
+            past.append(nxt)
+            out.append(nxt)
+            tok = nxt
+    finally:
+        capi.lib().th_llama_destroy(m)
+    return out
+
+
+def _device_sampled(dev, cfg, prompt, prefill, steps, seed, stop=None, **kw):
+    m = device_llama(dev, cfg, 7, 8, prefill)
+    s = capi.Sampler(capi.SamplingConfig(max_tokens=steps, stop_token=stop, **kw), seed=seed)
+    try:
+        pr = np.array(prompt, np.int32)
+        out = np.empty(steps, np.int32)
+        n = ctypes.c_size_t()
+        capi.check(capi.lib().th_llama_generate_sampled(m, s.handle, capi.ptr(pr), pr.size, prefill, capi.ptr(out),
+                                                        ctypes.byref(n)))
+    finally:
+        s.close()
+        capi.lib().th_llama_destroy(m)
+    return [int(t) for t in out[: n.value]]
+
+
+def test_small_llama_sampled_generation(dev):
+    """Non-greedy generate(): temperature, top-k, top-p and repetition
+    penalty on the host, every step on the device.  A categorical draw is
+    not a numerically stable function of the logits (a draw near a CDF
+    boundary flips with a 1e-6 change), so the pins are: the sampler equals
+    the oracle's on identical logits (test_sampling.py), the device logits
+    equal the oracle's (tests above), and here th_llama_generate_sampled
+    equals device steps fed through the oracle sampler, token for token,
+    with the stop token ending the run before it is appended
+    (sampling.rs:246-250)."""
+    cfg = CONFIG_SMALL
+    kw = dict(temperature=0.8, top_k=40, top_p=0.9, repetition_penalty=1.1)
+    prompt, prefill, steps = [3, 17, 1], 100, 24
+    want = _device_steps_oracle_sampler(dev, cfg, prompt, prefill, steps, 11, **kw)
+    got = _device_sampled(dev, cfg, prompt, prefill, steps, 11, **kw)
+    print("composed", want)
+    print("engine  ", got)
+    assert got == want and len(got) == steps and len(set(got)) > 3
+    stop = want[steps // 2]
+    got_stop = _device_sampled(dev, cfg, prompt, prefill, steps, 11, stop=stop, **kw)
+    assert got_stop == want[:want.index(stop)]
