@@ -117,6 +117,34 @@ int th_q4_download_blocks(const th_qweight* w, th_q4_block* blocks);
 int th_qweight_info(const th_qweight* w, size_t* rows, size_t* cols, int* bits);
 int th_qweight_free(th_qweight* w);
 
+/* quantize_matrix_q4 / quantize_matrix_q8 (quantize.rs:193-220) on the host:
+ * row-major f32 [rows][cols] -> rows*ceil(cols/32) reference blocks. */
+int th_quantize_q4(const float* data, size_t rows, size_t cols, th_q4_block* out);
+int th_quantize_q8(const float* data, size_t rows, size_t cols, th_q8_block* out);
+
+/* ---- safetensors weights ---------------------------------------------------
+ * The files tang-safetensors reads (crates/tang-safetensors/src/lib.rs:11-70):
+ * F64, F32, F16 and BF16 tensors; other dtypes are rejected, as there. */
+#define TH_ST_F64 0
+#define TH_ST_F32 1
+#define TH_ST_F16 2
+#define TH_ST_BF16 3
+typedef struct th_st_file th_st_file;
+int th_st_open(const char* path, th_st_file** out);
+int th_st_close(th_st_file* f);
+int th_st_count(const th_st_file* f, size_t* n);
+/* name stays valid until th_st_close; shape receives ndim values (max_dims room). */
+int th_st_info(const th_st_file* f, size_t index, const char** name, int* dtype, size_t* ndim, size_t* shape,
+               size_t max_dims);
+/* The tensor's values as f32 (exact from F16/BF16/F32; F64 rounded). */
+int th_st_read_f32(const th_st_file* f, const char* name, float* out, size_t n);
+/* Into a device buffer of dtype TH_F32, TH_BF16 or TH_F16 (RNE). */
+int th_st_upload(th_device* dev, const th_st_file* f, const char* name, th_dtype dtype, th_buffer** out);
+/* A 2-D tensor quantized with quantize_matrix_q4 / _q8 and uploaded in the
+ * device layout (f32 group scales). */
+int th_st_upload_q4(th_device* dev, const th_st_file* f, const char* name, th_qweight** out);
+int th_st_upload_q8(th_device* dev, const th_st_file* f, const char* name, th_qweight** out);
+
 /* ---- quantized linear ---------------------------------------------------
  * y[m][n] = sum_k x[m][k] * dequant(W)[n][k]: the quantized form of
  * ComputeDevice::matmul_b_transposed (device.rs:407) with B = W [n,k]

@@ -96,6 +96,16 @@ SIGNATURES = {
     "th_sampler_destroy": ([_P], _I),
     "th_sampler_sample": ([_P, _P, _S, _P, _S, _P], _I),
     "th_llama_generate_sampled": ([_P, _P, _P, _S, _S, _P, _P], _I),
+    "th_quantize_q4": ([_P, _S, _S, _P], _I),
+    "th_quantize_q8": ([_P, _S, _S, _P], _I),
+    "th_st_open": ([ctypes.c_char_p, _P], _I),
+    "th_st_close": ([_P], _I),
+    "th_st_count": ([_P, _P], _I),
+    "th_st_info": ([_P, _S, _P, _P, _P, _P, _S], _I),
+    "th_st_read_f32": ([_P, ctypes.c_char_p, _P, _S], _I),
+    "th_st_upload": ([_P, _P, ctypes.c_char_p, _I, _P], _I),
+    "th_st_upload_q4": ([_P, _P, ctypes.c_char_p, _P], _I),
+    "th_st_upload_q8": ([_P, _P, ctypes.c_char_p, _P], _I),
     "th_mla_decode": ([_P, _P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _F, _P], _I),
     "th_synth_seed": ([_U64, _U64, _U64], _U64),
     "th_synth_q4": ([_U64, _S, _S, _F, _F, _P, _P], _I),
@@ -179,11 +189,14 @@ def rope_tables(head_dim, max_seq, base):
 # --------------------------------------------------------------------------
 
 class Buffer:
-    def __init__(self, dev, dtype, n):
+    def __init__(self, dev, dtype, n, handle=None):
+        """Allocate n elements of dtype, or adopt a buffer handle the library
+        returned (which this object then frees)."""
         self.dev, self.dtype, self.n = dev, dtype, int(n)
-        h = ctypes.c_void_p()
-        check(lib().th_buffer_alloc(dev.handle, dtype, self.n, ctypes.byref(h)))
-        self.handle = h
+        if handle is None:
+            handle = ctypes.c_void_p()
+            check(lib().th_buffer_alloc(dev.handle, dtype, self.n, ctypes.byref(handle)))
+        self.handle = handle
 
     def __len__(self):
         return self.n
@@ -230,6 +243,72 @@ class QWeight:
         try:
             if self.handle and _lib is not None:
                 _lib.th_qweight_free(self.handle)
+        except Exception:
+            pass
+
+
+ST_DTYPES = {0: "F64", 1: "F32", 2: "F16", 3: "BF16"}
+
+
+def quantize_q4(data, rows, cols):
+    """quantize_matrix_q4 (quantize.rs:208) -> Q4_BLOCK records."""
+    a = np.ascontiguousarray(data, np.float32)
+    out = np.empty(rows * ((cols + 31) // 32), Q4_BLOCK)
+    check(lib().th_quantize_q4(ptr(a), rows, cols, ptr(out)))
+    return out
+
+
+def quantize_q8(data, rows, cols):
+    """quantize_matrix_q8 (quantize.rs:193) -> Q8_BLOCK records."""
+    a = np.ascontiguousarray(data, np.float32)
+    out = np.empty(rows * ((cols + 31) // 32), Q8_BLOCK)
+    check(lib().th_quantize_q8(ptr(a), rows, cols, ptr(out)))
+    return out
+
+
+class SafetensorsFile:
+    """th_st_* over one file: names, dtypes and shapes, f32 reads, uploads."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        check(lib().th_st_open(str(path).encode(), ctypes.byref(h)))
+        self.handle = h
+
+    def tensors(self):
+        n = ctypes.c_size_t()
+        check(lib().th_st_count(self.handle, ctypes.byref(n)))
+        out = {}
+        for i in range(n.value):
+            name, dt, nd = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_size_t()
+            shape = (ctypes.c_size_t * 16)()
+            check(lib().th_st_info(self.handle, i, ctypes.byref(name), ctypes.byref(dt), ctypes.byref(nd), shape, 16))
+            out[name.value.decode()] = (ST_DTYPES[dt.value], tuple(shape[j] for j in range(nd.value)))
+        return out
+
+    def read_f32(self, name, n):
+        out = np.empty(n, np.float32)
+        check(lib().th_st_read_f32(self.handle, name.encode(), ptr(out), n))
+        return out
+
+    def upload(self, dev, name, dtype=F32):
+        h = ctypes.c_void_p()
+        check(lib().th_st_upload(dev.handle, self.handle, name.encode(), dtype, ctypes.byref(h)))
+        return Buffer(dev, dtype, int(np.prod(self.tensors()[name][1], dtype=np.int64)), handle=h)
+
+    def upload_q4(self, dev, name):
+        h = ctypes.c_void_p()
+        check(lib().th_st_upload_q4(dev.handle, self.handle, name.encode(), ctypes.byref(h)))
+        rows, cols = self.tensors()[name][1]
+        return QWeight(h, rows, cols, 4)
+
+    def close(self):
+        if self.handle:
+            lib().th_st_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 
