@@ -121,6 +121,7 @@ def decode_bench(dev, steps):
         capi.check(L.th_llama_time_steps(h, 10, 2048, 8, ctypes.byref(ms)))  # warm (graph build)
         capi.check(L.th_llama_fill_kv_synthetic(h, 2048, 33))
         capi.check(L.th_llama_time_steps(h, 10, 2048, steps, ctypes.byref(ms)))
+        pf = prefill_7b(L, h, c)
     finally:
         L.th_llama_destroy(h)
     per_tok_ms = ms.value / steps
@@ -130,7 +131,23 @@ def decode_bench(dev, steps):
     return dict(tok_s=round(tok_s, 1), ms_per_token=round(per_tok_ms, 4), steps=steps,
                 bytes_per_token_mean=int(mean_bytes), roofline_tok_s=round(roof_tok_s, 1),
                 frac_of_roofline=round(tok_s / roof_tok_s, 4), kv_positions="2049..%d" % (2048 + steps),
-                init_s=round(init_s, 1))
+                init_s=round(init_s, 1), prefill=pf)
+
+
+def prefill_7b(L, h, c, n=512):
+    """th_llama_prefill of an n-token prompt at positions 0..n-1 (M=n int4
+    GEMMs on MFMA plus causal split attention), HIP events."""
+    import ctypes
+    toks = np.random.default_rng(0).integers(0, c["vocab"], n).astype(np.int32)
+    ms = ctypes.c_float()
+    capi.check(L.th_llama_time_prefill(h, capi.ptr(toks), n, 0, ctypes.byref(ms)))
+    d, ff, Ln = c["d_model"], c["d_ff"], c["n_layers"]
+    kvd = c["n_kv_heads"] * c["head_dim"]
+    lin = Ln * (d * (d + 2 * kvd) + d * d + 2 * d * ff + ff * d)
+    flops = 2.0 * n * lin + Ln * 2 * 2 * (n * (n + 1) / 2) * d  # linears + causal QK^T and PV
+    us = ms.value * 1e3
+    return dict(prompt_tokens=n, ms=round(ms.value, 2), tok_s=round(n / ms.value * 1e3, 1),
+                tflops=round(flops / us / 1e6, 1), frac_mfma_bf16=round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 4))
 
 
 MOE = dict(d=2048, ff=1408, E=64, S=2, k=6)

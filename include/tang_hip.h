@@ -231,6 +231,18 @@ int th_llama_set_token(th_llama* m, int32_t token);
  * on the device stream around the step launches. */
 int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, float* ms);
 
+/* Prefill: the prompt tokens[0..n) at positions pos..pos+n-1 run through
+ * every layer as M=n GEMMs (prompt chunks of up to 512 rows) with causal
+ * split attention, appending their K/V rows; then the last row's final norm,
+ * LM head and greedy argmax, as the decode step of smollm.rs:215-300 would
+ * give for tokens[n-1].  next_token / last_logits (vocab f32) are optional.
+ * The device state is left at position pos+n with next_token, so
+ * th_llama_generate(next_token, pos+n, ...) continues the sequence. */
+int th_llama_prefill(th_llama* m, const int32_t* tokens, size_t n, size_t pos, int32_t* next_token,
+                     float* last_logits);
+/* HIP-event time of one th_llama_prefill (after a warm-up call). */
+int th_llama_time_prefill(th_llama* m, const int32_t* tokens, size_t n, size_t pos, float* ms);
+
 /* ---- sampling (host, crates/tang-infer/src/sampling.rs) ------------------ */
 /* SamplingConfig (sampling.rs:6-20); stop_token < 0 means None. */
 typedef struct {

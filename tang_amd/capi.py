@@ -96,6 +96,8 @@ SIGNATURES = {
     "th_sampler_destroy": ([_P], _I),
     "th_sampler_sample": ([_P, _P, _S, _P, _S, _P], _I),
     "th_llama_generate_sampled": ([_P, _P, _P, _S, _S, _P, _P], _I),
+    "th_llama_prefill": ([_P, _P, _S, _S, _P, _P], _I),
+    "th_llama_time_prefill": ([_P, _P, _S, _S, _P], _I),
     "th_quantize_q4": ([_P, _S, _S, _P], _I),
     "th_quantize_q8": ([_P, _S, _S, _P], _I),
     "th_st_open": ([ctypes.c_char_p, _P], _I),

@@ -18,6 +18,7 @@
 // The whole step is captured once into a HIP graph that reads the position
 // and token from device memory: one graph launch per token, no host round
 // trip.
+#include <algorithm>
 #include <cstdlib>
 #include <vector>
 
@@ -174,6 +175,96 @@ __global__ __launch_bounds__(1024) void llama_argmax_kernel(const float* __restr
     }
 }
 
+// ---- prefill (a prompt chunk of n tokens at positions pos0..pos0+n-1) ----
+
+// Embedding rows (cpu.rs:151-168) into the f32 residual [n][d].
+__global__ void prefill_embed_kernel(const uint16_t* __restrict__ embed, const int32_t* __restrict__ tok, int d,
+                                     float* __restrict__ x) {
+    const int row = blockIdx.y;
+    const uint16_t* src = embed + (size_t)tok[row] * d;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
+        x[(size_t)row * d + i] = __uint_as_float((uint32_t)src[i] << 16);
+}
+
+// RMSNorm of one row to the bf16 linear input, with the decode engine's
+// rounding and summation order: per-16-element sums of squares, four per
+// lane, a fixed butterfly, then x * inv_rms * w (cpu.rs:126-149) rounded to
+// bf16 (cuda.rs:22).  One wave per row; d <= 4096.
+__global__ __launch_bounds__(64) void prefill_rmsnorm_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                            int d, float eps, uint16_t* __restrict__ out) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const float* xr = x + (size_t)row * d;
+    float part = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int t = lane + 64 * u;
+        float sq = 0.0f;
+        if (t * 16 < d)
+            for (int i = 0; i < 16; i++) {
+                const float v = xr[t * 16 + i];
+                sq += v * v;
+            }
+        part += sq;
+    }
+    const float tot = wave_sum(part);
+    const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+    for (int i = lane; i < d; i += 64)
+        out[(size_t)row * d + i] = f32_to_bf16_rne(xr[i] * inv * __uint_as_float((uint32_t)w[i] << 16));
+}
+
+// RoPE of q and k (device.rs:582-610, as EpiQKV) at position pos0 + row; q to
+// f32 [n][qd], k and v appended to the f16 cache rows.
+__global__ void prefill_rope_kv_kernel(const float* __restrict__ qkv, int pos0, const float* __restrict__ cs,
+                                       const float* __restrict__ sn, int qd, int kvd, int hd, float* __restrict__ q,
+                                       _Float16* __restrict__ kc, _Float16* __restrict__ vc) {
+    const int row = blockIdx.y, W = qd + 2 * kvd, pos = pos0 + row;
+    const float* src = qkv + (size_t)row * W;
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < W; n += gridDim.x * blockDim.x) {
+        float out = src[n];
+        if (n < qd + kvd) {
+            const int half = hd / 2, i = (n % hd) >> 1;
+            const float c = cs[(size_t)pos * half + i], s = sn[(size_t)pos * half + i];
+            out = (n & 1) == 0 ? src[n] * c - src[n + 1] * s : src[n - 1] * s + src[n] * c;
+        }
+        if (n < qd) q[(size_t)row * qd + n] = out;
+        else if (n < qd + kvd) kc[(size_t)pos * kvd + (n - qd)] = (_Float16)out;
+        else vc[(size_t)pos * kvd + (n - qd - kvd)] = (_Float16)out;
+    }
+}
+
+// x += y (device.rs:721, f32 residual).
+__global__ void prefill_add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        x[i] = x[i] + y[i];
+}
+
+// SwiGLU of the interleaved gate/up rows (tile b: gate 8b..8b+7, up
+// 8b..8b+7) to the bf16 down-projection input [n][ff].
+__global__ void prefill_swiglu_kernel(const float* __restrict__ gu, int ff, uint16_t* __restrict__ out) {
+    const int row = blockIdx.y;
+    const float* g = gu + (size_t)row * 2 * ff;
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < ff; j += gridDim.x * blockDim.x) {
+        const int b = j >> 3, rr = j & 7;
+        out[(size_t)row * ff + j] = f32_to_bf16_rne(swiglu_f64(g[16 * b + rr], g[16 * b + 8 + rr]));
+    }
+}
+
+// The last prompt row into the decode engine's residual, with the
+// per-16-element sums of squares its RMSNorm prologue reads.
+__global__ void prefill_last_row_kernel(const float* __restrict__ xrow, int d, float* __restrict__ x,
+                                        float* __restrict__ ssq) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t * 16 >= d) return;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float v = xrow[t * 16 + i];
+        x[t * 16 + i] = v;
+        s += v * v;
+    }
+    ssq[t] = s;
+}
+
 // One M=1 int4 GEMV of the engine: bf16 input (or the f32 residual through
 // the RMSNorm prologue when norm.ssq is set).  Small matrices split K over
 // eight waves per tile to keep enough weight bytes in flight.
@@ -224,6 +315,11 @@ struct th_llama {
     int32_t* history = nullptr;
     hipGraphExec_t graph = nullptr;
     bool weights_ready = false;
+    // prefill workspace (rows = prompt chunk), grown on demand
+    size_t pf_rows = 0;
+    float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_y = nullptr, *pf_gu = nullptr;
+    uint16_t *pf_xb = nullptr, *pf_att = nullptr, *pf_sg = nullptr;
+    int32_t* pf_tok = nullptr;
 };
 
 namespace th {
@@ -236,7 +332,8 @@ static void llama_free(th_llama* m) {
     if (m->lm) th_qweight_free(m->lm);
     void* ptrs[] = {m->embed, m->attn_norm, m->ffn_norm, m->final_norm, m->kcache, m->vcache, m->rope_cos,
                     m->rope_sin, m->x, m->q, m->logits, m->part, m->ssq, m->amax_v, m->att, m->sg, m->counters,
-                    m->amax_i, m->st, m->history};
+                    m->amax_i, m->st, m->history, m->pf_x, m->pf_qkv, m->pf_q, m->pf_y, m->pf_gu, m->pf_xb,
+                    m->pf_att, m->pf_sg, m->pf_tok};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
@@ -317,6 +414,72 @@ static void llama_launch_step(th_llama* m) {
     }
     llama_build_graph(m);
     TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+}
+
+constexpr size_t PREFILL_CHUNK = 512;  // prompt rows per pass (workspace ~100 MB at the 7B shape)
+
+static void prefill_reserve(th_llama* m, size_t rows) {
+    if (rows <= m->pf_rows) return;
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    void* old[] = {m->pf_x, m->pf_qkv, m->pf_q, m->pf_y, m->pf_gu, m->pf_xb, m->pf_att, m->pf_sg, m->pf_tok};
+    for (void* p : old)
+        if (p) (void)hipFree(p);
+    const th_llama_config& c = m->cfg;
+    const size_t d = c.d_model, ff = c.d_ff;
+    m->pf_x = dalloc<float>(rows * d);
+    m->pf_y = dalloc<float>(rows * d);
+    m->pf_qkv = dalloc<float>(rows * (m->qd + 2 * m->kvd));
+    m->pf_q = dalloc<float>(rows * m->qd);
+    m->pf_gu = dalloc<float>(rows * 2 * ff);
+    m->pf_xb = dalloc<uint16_t>(rows * d);
+    m->pf_att = dalloc<uint16_t>(rows * m->qd);
+    m->pf_sg = dalloc<uint16_t>(rows * ff);
+    m->pf_tok = dalloc<int32_t>(rows);
+    m->pf_rows = rows;
+}
+
+// One chunk of n prompt tokens at positions pos0.. through every layer; the
+// residual of its rows ends in pf_x.
+static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t pos0) {
+    const th_llama_config& c = m->cfg;
+    th_device* dev = m->dev;
+    hipStream_t s = dev->stream;
+    const int d = c.d_model, ff = c.d_ff, hd = c.head_dim, W = m->qd + 2 * m->kvd;
+    TH_HIP(hipMemcpyAsync(m->pf_tok, tok_host, n * 4, hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(prefill_embed_kernel, dim3(4, (unsigned)n), dim3(256), 0, s, m->embed, m->pf_tok, d, m->pf_x);
+    TH_LAUNCH_CHECK();
+    const size_t cache_layer = (size_t)c.max_seq * m->kvd;
+    // split attention: few enough splits that q_len * heads * splits records fit the scratch
+    const size_t attended = pos0 + n;
+    const int subs = (int)std::max<size_t>(1, ceil_div(attended, (size_t)ATTN_SUB * 8));
+    const int n_splits = (int)ceil_div(attended, (size_t)subs * ATTN_SUB);
+    for (int l = 0; l < c.n_layers; l++) {
+        _Float16* kc = m->kcache + l * cache_layer;
+        _Float16* vc = m->vcache + l * cache_layer;
+        hipLaunchKernelGGL(prefill_rmsnorm_kernel, dim3((unsigned)n), dim3(64), 0, s, m->pf_x,
+                           m->attn_norm + (size_t)l * d, d, c.eps, m->pf_xb);
+        TH_LAUNCH_CHECK();
+        launch_q4_linear(m->wqkv[l], m->pf_xb, TH_BF16, n, d, m->pf_qkv, W, s, dev);
+        hipLaunchKernelGGL(prefill_rope_kv_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_qkv, (int)pos0,
+                           m->rope_cos, m->rope_sin, m->qd, m->kvd, hd, m->pf_q, kc, vc);
+        TH_LAUNCH_CHECK();
+        float* part = (float*)device_scratch(dev, n * c.n_heads * n_splits * (hd + 2) * sizeof(float));
+        int* counters = device_counters(dev, n * c.n_heads);
+        launch_attn_split<true>(m->pf_q, kc, vc, true, (int)pos0, (int)n, c.n_heads, c.n_kv_heads, hd, subs, n_splits,
+                                part, counters, (void*)m->pf_att, nullptr, s);
+        launch_q4_linear(m->wo[l], m->pf_att, TH_BF16, n, m->qd, m->pf_y, d, s, dev);
+        hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
+        TH_LAUNCH_CHECK();
+        hipLaunchKernelGGL(prefill_rmsnorm_kernel, dim3((unsigned)n), dim3(64), 0, s, m->pf_x,
+                           m->ffn_norm + (size_t)l * d, d, c.eps, m->pf_xb);
+        TH_LAUNCH_CHECK();
+        launch_q4_linear(m->wgu[l], m->pf_xb, TH_BF16, n, d, m->pf_gu, 2 * ff, s, dev);
+        hipLaunchKernelGGL(prefill_swiglu_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_gu, ff, m->pf_sg);
+        TH_LAUNCH_CHECK();
+        launch_q4_linear(m->wd[l], m->pf_sg, TH_BF16, n, ff, m->pf_y, d, s, dev);
+        hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
+        TH_LAUNCH_CHECK();
+    }
 }
 
 // Concatenate rows of q4 matrices generated by th_synth_q4 (nib + f16 scales).
@@ -566,6 +729,52 @@ int th_llama_generate_sampled(th_llama* m, th_sampler* smp, const int32_t* promp
         TH_HIP(hipMemcpyAsync(&m->st->token, &next, sizeof next, hipMemcpyHostToDevice, s));
         TH_HIP(hipStreamSynchronize(s));
     }
+    TH_API_END
+}
+
+int th_llama_prefill(th_llama* m, const int32_t* tokens, size_t n, size_t pos, int32_t* next_token, float* last_logits) {
+    TH_API_BEGIN
+    TH_REQUIRE(m && m->weights_ready, "model not initialised");
+    TH_REQUIRE(tokens && n > 0, "empty prompt");
+    TH_REQUIRE(pos + n <= (size_t)m->cfg.max_seq, "prompt runs past max_seq");
+    for (size_t i = 0; i < n; i++) TH_REQUIRE(tokens[i] >= 0 && tokens[i] < m->cfg.vocab, "token out of range");
+    hipStream_t s = m->dev->stream;
+    prefill_reserve(m, std::min(n, PREFILL_CHUNK));
+    size_t rows = 0;
+    for (size_t c0 = 0; c0 < n; c0 += PREFILL_CHUNK) {
+        rows = std::min(PREFILL_CHUNK, n - c0);
+        prefill_chunk(m, tokens + c0, rows, pos + c0);
+        TH_HIP(hipStreamSynchronize(s));  // the token chunk is copied from the caller's memory
+    }
+    // the last row: final norm, LM head and argmax as a decode step would
+    const th_llama_config& c = m->cfg;
+    const int d = c.d_model;
+    LlamaState st{(int)(pos + n - 1), tokens[n - 1], 0, 0};
+    TH_HIP(hipMemcpyAsync(m->st, &st, sizeof st, hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(prefill_last_row_kernel, dim3((unsigned)ceil_div((size_t)d / 16, (size_t)256)), dim3(256), 0, s,
+                       m->pf_x + (rows - 1) * (size_t)d, d, m->x, m->ssq);
+    TH_LAUNCH_CHECK();
+    NormArgs fin;
+    fin.ssq = m->ssq; fin.nssq = d / 16; fin.w = m->final_norm; fin.eps = c.eps;
+    gemv_engine<true>(m->lm, m->x, fin, EpiTileMax{m->logits, m->amax_v, m->amax_i, c.vocab}, s);
+    hipLaunchKernelGGL(llama_argmax_kernel, dim3(1), dim3(1024), 0, s, m->amax_v, m->amax_i,
+                       (int)ceil_div((size_t)c.vocab, 16), m->st, m->history);
+    TH_LAUNCH_CHECK();
+    TH_HIP(hipStreamSynchronize(s));
+    if (next_token) TH_HIP(hipMemcpy(next_token, m->history, 4, hipMemcpyDeviceToHost));
+    if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost));
+    TH_API_END
+}
+
+int th_llama_time_prefill(th_llama* m, const int32_t* tokens, size_t n, size_t pos, float* ms) {
+    TH_API_BEGIN
+    TH_REQUIRE(m && ms, "null argument");
+    check_status(th_llama_prefill(m, tokens, n, pos, nullptr, nullptr));  // warm: workspace, scratch
+    TH_HIP(hipEventRecord(m->dev->ev_start, m->dev->stream));
+    check_status(th_llama_prefill(m, tokens, n, pos, nullptr, nullptr));
+    TH_HIP(hipEventRecord(m->dev->ev_stop, m->dev->stream));
+    TH_HIP(hipEventSynchronize(m->dev->ev_stop));
+    TH_HIP(hipEventElapsedTime(ms, m->dev->ev_start, m->dev->ev_stop));
     TH_API_END
 }
 

@@ -193,3 +193,40 @@ def test_small_llama_sampled_generation(dev):
     stop = want[steps // 2]
     got_stop = _device_sampled(dev, cfg, prompt, prefill, steps, 11, stop=stop, **kw)
     assert got_stop == want[:want.index(stop)]
+
+
+def _prefill(m, cfg, toks, pos):
+    pr = np.array(toks, np.int32)
+    nxt = ctypes.c_int32()
+    logits = np.empty(cfg["vocab"], np.float32)
+    capi.check(capi.lib().th_llama_prefill(m, capi.ptr(pr), pr.size, pos, ctypes.byref(nxt), capi.ptr(logits)))
+    return nxt.value, logits
+
+
+@pytest.mark.parametrize("n", [1, 37, 600])  # 600: two prompt chunks of the M=n GEMM path
+def test_small_llama_prefill_matches_oracle(dev, n):
+    """th_llama_prefill (M=n GEMMs, causal split attention, K/V appended)
+    against the oracle fed the same tokens one decode step at a time: the
+    last logits within the bf16-activation bar, the same next token, and 12
+    greedy decode steps continuing from the state prefill leaves (which
+    read the K/V rows prefill wrote) match the oracle's continuation."""
+    cfg = dict(CONFIG_SMALL, max_seq=max(CONFIG_SMALL["max_seq"], 100 + n + 16))
+    prefill, steps = 100, 12
+    print(f"prefill n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    toks = [int(t) for t in rng.integers(0, cfg["vocab"], n)]
+    ref = OracleLlama(cfg, 7, 8, prefill)
+    for i, t in enumerate(toks):
+        r_next, r_logits = ref.step(t, prefill + i)
+    r_cont, _, _ = ref.generate(int(r_next), prefill + n, steps)
+    m = device_llama(dev, cfg, 7, 8, prefill)
+    try:
+        nxt, logits = _prefill(m, cfg, toks, prefill)
+        cont, _ = device_generate(m, cfg, nxt, prefill + n, steps)
+    finally:
+        capi.lib().th_llama_destroy(m)
+    err = max_abs_rel(logits, r_logits)
+    print("max_abs_rel", err, "next", nxt, int(r_next))
+    assert err < 2e-2
+    assert nxt == int(r_next)
+    assert list(cont) == r_cont
