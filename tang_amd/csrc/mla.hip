@@ -15,10 +15,10 @@
 //      scores on v_mfma_f32_16x16x32_bf16 (heads x positions; each wave owns
 //      a quarter of the k-steps and keeps its A operand in registers; partial
 //      scores are summed in LDS), online softmax per head, then P.C on the
-//      same MFMA (P as hi + lo bf16, C exact bf16); the per-split
-//      {max, sum, o_lat} records are then merged by a small kernel with one
-//      workgroup per (sequence, head);
-//   3. up-projection through W_UV.
+//      same MFMA (P as hi + lo bf16, C exact bf16), one {max, sum, o_lat}
+//      record per split;
+//   3. per (head, sequence): the split merge in LDS, then the up-projection
+//      through W_UV.
 // The cache dominates the traffic: B*L*(r+dr)*2 bytes.
 #include <mutex>
 #include <utility>
@@ -344,24 +344,27 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
     }
 }
 
-// o_lat[b][h] = sum_s w_s acc_s / sum_s w_s l_s with w_s = exp(m_s - max m).
-// Workgroup (sequence, head, 128 latent dims); thread (dim, quarter of the
-// splits), quarters summed in order.
-__global__ __launch_bounds__(512) void mla_merge_kernel(const float* __restrict__ part, int n_splits, int R,
-                                                        float* __restrict__ o_lat) {
+// Split merge fused with the W_UV up-projection: workgroup (head h,
+// sequence b).  o_lat[b][h] = sum_s w_s acc_s / sum_s w_s l_s (split order,
+// w_s = exp(m_s - max m)) is built in LDS, then out[b][h][n] = scale_n *
+// sum_k W_UV[h*dv + n][k] o_lat[k]: thread (row n, half of k), halves summed
+// in order.  r <= 512, dv <= 128, n_splits <= 64.
+constexpr int MLA_UP_THREADS = 256;
+
+__global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const float* __restrict__ part, int n_splits,
+                                                                     int R, const uint8_t* __restrict__ wq,
+                                                                     const float* __restrict__ wsc, int dv, int Kp,
+                                                                     float* __restrict__ out) {
+    __shared__ float olat[512];
     __shared__ float wts[64];
     __shared__ float Lsh;
-    __shared__ float sum4[4][128];
-    const int b = blockIdx.x, hh = blockIdx.y, tid = threadIdx.x;
-    const int d = blockIdx.z * 128 + (tid & 127), g = tid >> 7;
+    __shared__ float half_sum[2][128];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const float* recs = part + (size_t)b * n_splits * MLA_H * (R + 2);
-    const int per = (n_splits + 3) / 4, s0 = g * per, s1 = min(n_splits, s0 + per);
-    const int dd = min(d, R - 1);
-    float v[16];  // issued before the (dependent) max / sum phase
-#pragma unroll
-    for (int i = 0; i < 16; i++) v[i] = recs[((size_t)min(s0 + i, n_splits - 1) * MLA_H + hh) * (R + 2) + 2 + dd];
+    // every record value this thread needs, issued before the max / sum phase
+    constexpr int DPT = 2, SB = 16;  // dims per thread, splits per load round
     if (tid < 64) {
-        const float* rec = recs + ((size_t)min(tid, n_splits - 1) * MLA_H + hh) * (R + 2);
+        const float* rec = recs + ((size_t)min(tid, n_splits - 1) * MLA_H + h) * (R + 2);
         const float m = tid < n_splits ? rec[0] : -INFINITY;
         const float l = tid < n_splits ? rec[1] : 0.0f;
         float M = m;
@@ -373,14 +376,47 @@ __global__ __launch_bounds__(512) void mla_merge_kernel(const float* __restrict_
         if (tid == 0) Lsh = L;
     }
     __syncthreads();
-    float a = 0.0f;
+    float a[DPT] = {0.0f, 0.0f};
+    for (int s0 = 0; s0 < n_splits; s0 += SB) {
+        float v[SB][DPT];
 #pragma unroll
-    for (int i = 0; i < 16; i++) a += s0 + i < s1 ? v[i] * wts[s0 + i] : 0.0f;
-    sum4[g][tid & 127] = a;
+        for (int i = 0; i < SB; i++)
+#pragma unroll
+            for (int j = 0; j < DPT; j++) {
+                const int d = min(tid + 256 * j, R - 1);
+                v[i][j] = recs[((size_t)min(s0 + i, n_splits - 1) * MLA_H + h) * (R + 2) + 2 + d];
+            }
+#pragma unroll
+        for (int i = 0; i < SB; i++)
+#pragma unroll
+            for (int j = 0; j < DPT; j++) a[j] += s0 + i < n_splits ? v[i][j] * wts[s0 + i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < DPT; j++)
+        if (tid + 256 * j < R) olat[tid + 256 * j] = a[j] / Lsh;
     __syncthreads();
-    if (g == 0 && d < R)
-        o_lat[((size_t)b * MLA_H + hh) * R + d] =
-            (((sum4[0][tid] + sum4[1][tid]) + sum4[2][tid]) + sum4[3][tid]) / Lsh;
+    // up-projection through the q8 tiles (16 rows x 64 k, lane q*16+r holds k 16q..16q+15 of row r)
+    const int n = tid & 127, kh = tid >> 7, NCH = Kp >> 6;
+    const int row = h * dv + min(n, dv - 1), t = row >> 4, r = row & 15;
+    const int c0 = kh * ((NCH + 1) / 2), c1 = min(NCH, c0 + (NCH + 1) / 2);
+    float acc = 0.0f;
+    for (int c = c0; c < c1; c++) {
+        uint4 w4[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) w4[q] = *(const uint4*)(wq + (((size_t)t * NCH + c) * 64 + q * 16 + r) * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t ww[4] = {w4[q].x, w4[q].y, w4[q].z, w4[q].w};
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int k = c * 64 + q * 16 + e;
+                acc = __builtin_fmaf((float)(int8_t)(ww[e >> 2] >> (8 * (e & 3))), k < R ? olat[k] : 0.0f, acc);
+            }
+        }
+    }
+    half_sum[kh][n] = acc;
+    __syncthreads();
+    if (tid < dv) out[((size_t)b * MLA_H + h) * dv + tid] = (half_sum[0][tid] + half_sum[1][tid]) * wsc[h * dv + tid];
 }
 
 static size_t head_gemv_lds(size_t B, size_t Kp) { return (B * (Kp / 16) * 20 + B * 256) * 4; }
@@ -434,7 +470,7 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     TH_REQUIRE(L > 0 && B > 0 && B <= 16, "1 <= B <= 16 sequences");
     TH_REQUIRE(w_uk->bits == 8 && w_uk->per_row && w_uk->rows == H * r && w_uk->cols == dn, "w_uk must be q8 rowwise [H*r][dn]");
     TH_REQUIRE(w_uv->bits == 8 && w_uv->per_row && w_uv->rows == H * dv && w_uv->cols == r, "w_uv must be q8 rowwise [H*dv][r]");
-    TH_REQUIRE(r % 16 == 0 && dv % 16 == 0, "r and dv must be multiples of 16");
+    TH_REQUIRE(r % 16 == 0 && dv % 16 == 0 && dv <= 128, "r and dv must be multiples of 16, dv <= 128");
     require_len(q_nope, TH_F32, B * H * dn, "q_nope");
     require_len(q_rope, TH_F32, B * H * dr, "q_rope");
     require_len(cache, TH_BF16, B * L * (r + dr), "cache");
@@ -448,11 +484,9 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     // workspace: A operand, split records, o_lat
     const size_t qa_bytes = B * 2 * H * W * 2;
     const size_t part_bytes = B * (size_t)n_splits * H * (r + 2) * 4;
-    const size_t olat_bytes = B * H * r * 4;
-    char* ws = (char*)device_scratch(dev, round_up(qa_bytes, 256) + round_up(part_bytes, 256) + olat_bytes);
+    char* ws = (char*)device_scratch(dev, round_up(qa_bytes, 256) + part_bytes);
     uint16_t* qa = (uint16_t*)ws;
     float* part = (float*)(ws + round_up(qa_bytes, 256));
-    float* olat = (float*)(ws + round_up(qa_bytes, 256) + round_up(part_bytes, 256));
     // 1. absorb
     hipLaunchKernelGGL(mla_q8_heads_kernel<0>, dim3((unsigned)H, (unsigned)(r / 16)), dim3(256), head_gemv_lds(B, w_uk->Kp), s,
                        (const uint8_t*)w_uk->data, (const float*)w_uk->scales, (int)r, (int)dn, (int)w_uk->Kp, (int)B,
@@ -466,14 +500,10 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     launch_mla_attn(W, dim3((unsigned)B, (unsigned)n_splits), lds, s, qa, (const uint16_t*)cache->ptr, (int)L, (int)r,
                     sm_scale, n_splits, part);
     TH_LAUNCH_CHECK();
-    hipLaunchKernelGGL(mla_merge_kernel, dim3((unsigned)B, (unsigned)H, (unsigned)ceil_div(r, (size_t)128)), dim3(512), 0,
-                       s, part, n_splits, (int)r, olat);
-    TH_LAUNCH_CHECK();
-    // 3. up-projection
-    hipLaunchKernelGGL(mla_q8_heads_kernel<1>, dim3((unsigned)H, (unsigned)(dv / 16)), dim3(256), head_gemv_lds(B, w_uv->Kp), s,
-                       (const uint8_t*)w_uv->data, (const float*)w_uv->scales, (int)dv, (int)r, (int)w_uv->Kp, (int)B,
-                       (int)H, olat, (int)(H * r), (int)r, (float*)out->ptr, (uint16_t*)nullptr, (const float*)nullptr,
-                       0);
+    // 3. merge + up-projection
+    hipLaunchKernelGGL(mla_merge_up_kernel, dim3((unsigned)H, (unsigned)B), dim3(MLA_UP_THREADS), 0, s, part, n_splits,
+                       (int)r, (const uint8_t*)w_uv->data, (const float*)w_uv->scales, (int)dv, (int)w_uv->Kp,
+                       (float*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
 }
