@@ -224,25 +224,34 @@ __global__ __launch_bounds__(1024) void moe_dispatch_kernel(const int32_t* __res
 }
 
 // Grouped GEMV source: workgroup -> (work item, tile of that expert's matrix).
+// A workgroup takes MOE_TPW consecutive tiles of one work item's expert, so
+// the work item -> expert -> weights lookup and the activation staging are
+// paid once per MOE_TPW tiles.
+constexpr int MOE_TPW = 8;
+
 struct MoeSrc {
     static constexpr bool GROUPED = true;
+    static constexpr int TPW = MOE_TPW;
     const MoeWork* work;
     const uint4* const* wdata;
     const _Float16* const* wscales;
     const int* slot_token;  // null: activation rows are the slots themselves
-    int tiles;
-    int slot0 = 0;
+    int tiles;              // 16-row tiles per expert matrix
+    int wg_per_item;        // ceil(tiles / TPW)
+    int slot0 = 0, nt = 1;
     template <typename ST>
     __device__ __forceinline__ bool select(int bid, const uint4*& wt, const ST*& sc, int& t, int& mrows) {
-        const MoeWork w = work[bid / tiles];
+        const MoeWork w = work[bid / wg_per_item];
         if (w.expert < 0) return false;
-        t = bid % tiles;
+        t = (bid % wg_per_item) * TPW;
+        nt = min(TPW, tiles - t);
         wt = wdata[w.expert];
         sc = (const ST*)wscales[w.expert];
         mrows = w.rows;
         slot0 = w.slot0;
         return true;
     }
+    __device__ __forceinline__ int tiles_here() const { return nt; }
     __device__ __forceinline__ int x_row(int m) const { return slot_token ? slot_token[slot0 + m] : slot0 + m; }
     __device__ __forceinline__ int out_row(int m) const { return slot0 + m; }
 };
@@ -419,12 +428,13 @@ static void moe_grouped_gemv(const th_moe* m, const th_qweight* w0, const uint4*
                              const _Float16* const* scales, const uint16_t* x, const int* slot_token, size_t max_work,
                              Epi epi) {
     const int tiles = (int)(w0->Np / 16);
-    MoeSrc src{m->work, data, scales, slot_token, tiles};
+    const int wg_per_item = (tiles + MOE_TPW - 1) / MOE_TPW;
+    MoeSrc src{m->work, data, scales, slot_token, tiles, wg_per_item};
     const size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w0->Kp / 128));
     TH_REQUIRE(smem <= 160 * 1024, "MoE GEMV LDS above 160 KiB");
     // Expert matrices are short (K = 2048 is 16 items of 128): every item of
     // a wave in flight at once.
-    auto k = q4_gemv_kernel<MR, false, true, _Float16, Epi, 4, (MR <= 8 ? 4 : 2), NW, false, MoeSrc>;
+    auto k = q4_gemv_kernel<MR, false, true, _Float16, Epi, 4, (MR <= 8 ? 3 : 2), NW, false, MoeSrc>;
     static std::mutex mu;
     static size_t done = 0;
     {
@@ -434,7 +444,7 @@ static void moe_grouped_gemv(const th_moe* m, const th_qweight* w0, const uint4*
             done = smem;
         }
     }
-    hipLaunchKernelGGL(k, dim3((unsigned)(max_work * tiles)), dim3(64 * NW), smem, m->dev->stream, (const uint4*)nullptr,
+    hipLaunchKernelGGL(k, dim3((unsigned)(max_work * wg_per_item)), dim3(64 * NW), smem, m->dev->stream, (const uint4*)nullptr,
                        (const _Float16*)nullptr, (const void*)x, (int)w0->cols, (int)w0->Kp, (int)w0->rows,
                        (int)w0->cols, epi, NormArgs{}, src);
     TH_LAUNCH_CHECK();

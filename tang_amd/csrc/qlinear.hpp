@@ -215,6 +215,7 @@ struct Q4GemvSmem {
 // number of live rows and the gathered activation / output rows.
 struct SingleMatrix {
     static constexpr bool GROUPED = false;
+    static constexpr int TPW = 1;  // tiles per workgroup
     template <typename ST>
     __device__ __forceinline__ bool select(int bid, const uint4*& wt, const ST*& sc, int& t, int& mrows) {
         t = bid;
@@ -342,11 +343,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 
     const uint4* wp = wt + (size_t)t * GQ * 64 + lane;
     auto item_gq = [&](int i) { return i < nmine ? wave + NW * i : 0; };
-    auto scale_ptr = [&](int i) -> const typename SR::Rec* {
+    auto scale_ptr_t = [&](int i, int tile) -> const typename SR::Rec* {
         const int gq = item_gq(i);  // past the end: a valid record of this tile
         const int g0 = (F16S && NW == 4) ? (gq & ~4) : gq;
-        return (const typename SR::Rec*)(sc + q4_scale_index(F16S, t, g0, r, 0, GQ));
+        return (const typename SR::Rec*)(sc + q4_scale_index(F16S, tile, g0, r, 0, GQ));
     };
+    auto scale_ptr = [&](int i) { return scale_ptr_t(i, t); };
+    // tiles of this workgroup: t, t+1, ... (one unless the source groups them)
+    int ntl = 1;
+    if constexpr (Src::TPW > 1) ntl = src.tiles_here();
 
     // 1. activations for this wave's groups.  Task (item i, group j, row m)
     //    covers the 32 values of one group; its four 8-value chunks go to
@@ -500,12 +505,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     constexpr int ACC = MR < 4 ? MR : 4;
     // A rows >= MR and C rows >= MR only feed D rows that are discarded, so
     // those lanes read real (finite) data of another row: no masking needed.
     const uint4* abase = xw + (size_t)(r < mr_live ? r : 0) * 4 + q;
     const float* cbase = bw + 4 * (q & (BS / 4 - 1));
+    for (int tt = 0; tt < ntl; tt++) {  // one trip unless the source groups tiles
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float4_t dprev = {0.0f, 0.0f, 0.0f, 0.0f};
     float sprev = 0.0f;
 
@@ -553,6 +559,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     }
 #pragma unroll
     for (int e = 0; e < ACC; e++) acc[e] = __builtin_fmaf(sprev, dprev[e], acc[e]);
+    if constexpr (Src::TPW > 1) {
+        // the next tile's first items stream in during this tile's reduction;
+        // branch-free: the last tile re-reads its own first items (cache hits)
+        const int tn = tt + 1 < ntl ? t + 1 : t;
+        const uint4* wpn = wt + (size_t)tn * GQ * 64 + lane;
+#pragma unroll
+        for (int u = 0; u < D; u++) wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
+#pragma unroll
+        for (int vv = 0; vv < NS; vv++) sbuf[vv] = *scale_ptr_t(vv * SI, tn);
+    }
 
     // lane (q, r) holds D rows 4q..4q+3 of column r
     if (q * 4 < MR) {
@@ -581,6 +597,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         __syncthreads();
         epi.finish(t, (int)gridDim.x, aux, tid);
     }
+    if constexpr (Src::TPW > 1) {
+        __syncthreads();  // red and tilev are rewritten by the next tile
+        t += 1;
+        wp = wt + (size_t)t * GQ * 64 + lane;
+    }
+    }  // tiles
 }
 
 // ---------------------------------------------------------------------------
