@@ -225,6 +225,21 @@ struct SingleMatrix {
     __device__ __forceinline__ int out_row(int m) const { return m; }
 };
 
+// One matrix, TPW consecutive tiles per workgroup (activations staged once).
+template <int TPWv>
+struct SingleMatrixTiles : SingleMatrix {
+    static constexpr int TPW = TPWv;
+    int tiles;  // 16-row tiles of the matrix
+    int nt = 1;
+    template <typename ST>
+    __device__ __forceinline__ bool select(int bid, const uint4*& wt, const ST*& sc, int& t, int& mrows) {
+        t = bid * TPW;
+        nt = min(TPW, tiles - t);
+        return true;
+    }
+    __device__ __forceinline__ int tiles_here() const { return nt; }
+};
+
 // One matrix with fewer live activation rows than the kernel's tile rows
 // (a run-time row count costs the staging its constant-folded indexing, so
 // only the ragged launches use it).
