@@ -347,22 +347,39 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
 // Split merge fused with the W_UV up-projection: workgroup (head h,
 // sequence b).  o_lat[b][h] = sum_s w_s acc_s / sum_s w_s l_s (split order,
 // w_s = exp(m_s - max m)) is built in LDS, then out[b][h][n] = scale_n *
-// sum_k W_UV[h*dv + n][k] o_lat[k]: thread (row n, half of k), halves summed
-// in order.  r <= 512, dv <= 128, n_splits <= 64.
+// sum_k W_UV[h*dv + n][k] o_lat[k]: thread (row n, half of the 64-k chunks),
+// halves summed in order; the W_UV and record loads are all issued at the
+// start.  r <= 512, dv <= 128, n_splits <= 64.
 constexpr int MLA_UP_THREADS = 256;
 
 __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const float* __restrict__ part, int n_splits,
                                                                      int R, const uint8_t* __restrict__ wq,
                                                                      const float* __restrict__ wsc, int dv, int Kp,
                                                                      float* __restrict__ out) {
-    __shared__ float olat[512];
+    __shared__ __align__(16) float olat[512];
     __shared__ float wts[64];
     __shared__ float Lsh;
     __shared__ float half_sum[2][128];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const float* recs = part + (size_t)b * n_splits * MLA_H * (R + 2);
-    // every record value this thread needs, issued before the max / sum phase
-    constexpr int DPT = 2, SB = 16;  // dims per thread, splits per load round
+    constexpr int DPT = 2, SB = 32;    // dims per thread, splits per load round
+    constexpr int CPT = 4;             // 64-k chunks of W_UV per thread (r <= 512)
+    // the up-projection's weights do not depend on the merge: load them first
+    const int n = tid & 127, kh = tid >> 7, NCH = Kp >> 6;
+    const int row = h * dv + min(n, dv - 1), t = row >> 4, r = row & 15;
+    uint4 w4[CPT][4];
+#pragma unroll
+    for (int ci = 0; ci < CPT; ci++) {
+        const int c = min(kh * CPT + ci, NCH - 1);  // chunks past K: loaded, multiplied by zero below
+#pragma unroll
+        for (int q = 0; q < 4; q++) w4[ci][q] = *(const uint4*)(wq + (((size_t)t * NCH + c) * 64 + q * 16 + r) * 16);
+    }
+    float v[SB][DPT];
+#pragma unroll
+    for (int i = 0; i < SB; i++)
+#pragma unroll
+        for (int j = 0; j < DPT; j++)
+            v[i][j] = recs[((size_t)min(i, n_splits - 1) * MLA_H + h) * (R + 2) + 2 + min(tid + 256 * j, R - 1)];
     if (tid < 64) {
         const float* rec = recs + ((size_t)min(tid, n_splits - 1) * MLA_H + h) * (R + 2);
         const float m = tid < n_splits ? rec[0] : -INFINITY;
@@ -377,40 +394,40 @@ __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const floa
     }
     __syncthreads();
     float a[DPT] = {0.0f, 0.0f};
-    for (int s0 = 0; s0 < n_splits; s0 += SB) {
-        float v[SB][DPT];
+#pragma unroll
+    for (int i = 0; i < SB; i++)
+#pragma unroll
+        for (int j = 0; j < DPT; j++) a[j] += i < n_splits ? v[i][j] * wts[i] : 0.0f;
+    for (int s0 = SB; s0 < n_splits; s0 += SB) {  // beyond 32 splits: further rounds
 #pragma unroll
         for (int i = 0; i < SB; i++)
 #pragma unroll
-            for (int j = 0; j < DPT; j++) {
-                const int d = min(tid + 256 * j, R - 1);
-                v[i][j] = recs[((size_t)min(s0 + i, n_splits - 1) * MLA_H + h) * (R + 2) + 2 + d];
-            }
+            for (int j = 0; j < DPT; j++)
+                v[i][j] = recs[((size_t)min(s0 + i, n_splits - 1) * MLA_H + h) * (R + 2) + 2 + min(tid + 256 * j, R - 1)];
 #pragma unroll
         for (int i = 0; i < SB; i++)
 #pragma unroll
             for (int j = 0; j < DPT; j++) a[j] += s0 + i < n_splits ? v[i][j] * wts[s0 + i] : 0.0f;
     }
 #pragma unroll
-    for (int j = 0; j < DPT; j++)
-        if (tid + 256 * j < R) olat[tid + 256 * j] = a[j] / Lsh;
+    for (int j = 0; j < DPT; j++) olat[tid + 256 * j] = tid + 256 * j < R ? a[j] / Lsh : 0.0f;
     __syncthreads();
-    // up-projection through the q8 tiles (16 rows x 64 k, lane q*16+r holds k 16q..16q+15 of row r)
-    const int n = tid & 127, kh = tid >> 7, NCH = Kp >> 6;
-    const int row = h * dv + min(n, dv - 1), t = row >> 4, r = row & 15;
-    const int c0 = kh * ((NCH + 1) / 2), c1 = min(NCH, c0 + (NCH + 1) / 2);
+    // out[n] = scale_n * sum_k W_UV[n][k] o_lat[k]; thread (row n, half kh of the chunks)
     float acc = 0.0f;
-    for (int c = c0; c < c1; c++) {
-        uint4 w4[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) w4[q] = *(const uint4*)(wq + (((size_t)t * NCH + c) * 64 + q * 16 + r) * 16);
+    for (int ci = 0; ci < CPT; ci++) {
+        const int c = kh * CPT + ci;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const uint32_t ww[4] = {w4[q].x, w4[q].y, w4[q].z, w4[q].w};
+            const uint32_t ww[4] = {w4[ci][q].x, w4[ci][q].y, w4[ci][q].z, w4[ci][q].w};
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int k = c * 64 + q * 16 + e;
-                acc = __builtin_fmaf((float)(int8_t)(ww[e >> 2] >> (8 * (e & 3))), k < R ? olat[k] : 0.0f, acc);
+            for (int e4 = 0; e4 < 4; e4++) {
+                const int k0 = c * 64 + q * 16 + e4 * 4;  // olat is zero past R (cleared below), 512 entries
+                const float4 o = (c < NCH) ? *(const float4*)&olat[min(k0, 508)] : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    acc = __builtin_fmaf((float)(int8_t)(ww[e4] >> (8 * e)), ov[e], acc);
             }
         }
     }
