@@ -71,15 +71,45 @@ static void q4_gemv_dispatch(const th_qweight* w, const void* x, size_t m, size_
         case 2: q4_gemv_launch<2, XF32, ST>(w, x, ldx, y, ldy, s); break;
         case 3: q4_gemv_launch<3, XF32, ST>(w, x, ldx, y, ldy, s); break;
         case 4: q4_gemv_launch<4, XF32, ST>(w, x, ldx, y, ldy, s); break;
-        case 5: case 6: case 7: case 8:  // bf16 rows only: an 8-row tile, live rows = m
-            if constexpr (!XF32) {
-                SingleMatrixRows src;
-                src.rows = (int)m;
-                q4_gemv_launch<8, false, ST, SingleMatrixRows>(w, x, ldx, y, ldy, s, src);
-                break;
-            }
-            [[fallthrough]];
         default: throw Error(TH_ERR_INVALID, "q4 gemv: m out of range");
+    }
+}
+
+// M block rows (8 or 16 staged rows after f32 hi/lo splitting), m of them
+// live: NW waves split K, and each workgroup takes ceil(tiles / CUs)
+// consecutive tiles so that the whole grid is resident at once and the
+// staged activations are read once per workgroup.
+template <int M, bool XF32, typename ST, bool VEC, bool RT>
+static void q4_span_launch_v(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
+                             hipStream_t s, int cus) {
+    constexpr int MR = XF32 ? 2 * M : M;
+    constexpr int NW = MR >= 16 ? 16 : 8, WPE = MR >= 16 ? 1 : 4;
+    using Src = SingleMatrixSpan<RT>;
+    const int tiles = (int)(w->Np / 16);
+    Src src;
+    src.tiles = tiles;
+    src.per = (int)ceil_div((size_t)tiles, (size_t)cus);
+    src.rows = (int)m;
+    const unsigned grid = (unsigned)ceil_div((size_t)tiles, (size_t)src.per);
+    const size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w->Kp / 128));
+    TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
+    auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src>;
+    set_smem(k, smem);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * NW), smem, s, (const uint4*)w->data, (const ST*)w->scales, x,
+                       (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, EpiStore{y, (int)ldy}, NormArgs{}, src);
+    TH_LAUNCH_CHECK();
+}
+
+template <int M, bool XF32, typename ST>
+static void q4_span_launch(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
+                           hipStream_t s, int cus) {
+    const bool vec = x_vec_ok(x, ldx, w->cols);
+    if (m == M) {  // all rows live: constant-folded staging
+        if (vec) q4_span_launch_v<M, XF32, ST, true, false>(w, x, m, ldx, y, ldy, s, cus);
+        else q4_span_launch_v<M, XF32, ST, false, false>(w, x, m, ldx, y, ldy, s, cus);
+    } else {
+        if (vec) q4_span_launch_v<M, XF32, ST, true, true>(w, x, m, ldx, y, ldy, s, cus);
+        else q4_span_launch_v<M, XF32, ST, false, true>(w, x, m, ldx, y, ldy, s, cus);
     }
 }
 
@@ -132,8 +162,13 @@ static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t 
 template <bool XF32, typename ST>
 static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
                         hipStream_t s, th_device* dev) {
-    const bool tile8_fits = Q4GemvSmem<8, 8>::bytes((int)(w->Kp / 128)) <= 160 * 1024;  // staged rows fit LDS
-    if (m <= 4 || (!XF32 && m <= 8 && tile8_fits)) q4_gemv_dispatch<XF32, ST>(w, x, m, ldx, y, ldy, s);
+    const int GQ = (int)(w->Kp / 128), cus = dev && dev->num_cus > 0 ? dev->num_cus : 256;
+    const bool fits8 = Q4GemvSmem<8, 8>::bytes(GQ) <= 160 * 1024;    // staged rows fit LDS
+    const bool fits16 = Q4GemvSmem<16, 16>::bytes(GQ) <= 160 * 1024;
+    if (m <= 4) q4_gemv_dispatch<XF32, ST>(w, x, m, ldx, y, ldy, s);
+    else if (XF32 && m <= 8 && fits16) q4_span_launch<8, true, ST>(w, x, m, ldx, y, ldy, s, cus);
+    else if (!XF32 && m <= 8 && fits8) q4_span_launch<8, false, ST>(w, x, m, ldx, y, ldy, s, cus);
+    else if (!XF32 && m <= 16 && fits16) q4_span_launch<16, false, ST>(w, x, m, ldx, y, ldy, s, cus);
     else if (m <= 16) q4_mfma_launch<1, 1, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
     else q4_mfma_launch<2, 4, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
 }

@@ -240,17 +240,23 @@ struct SingleMatrixTiles : SingleMatrix {
     __device__ __forceinline__ int tiles_here() const { return nt; }
 };
 
-// One matrix with fewer live activation rows than the kernel's tile rows
-// (a run-time row count costs the staging its constant-folded indexing, so
-// only the ragged launches use it).
-struct SingleMatrixRows : SingleMatrix {
-    int rows;
+// One matrix, `per` consecutive tiles per workgroup (chosen so that the grid
+// is one round of the chip: a staged 8/16-row activation block is then read
+// from HBM once per CU, not once per tile), with `rows` live activation rows
+// when RT_ROWS (otherwise the kernel's constant row count).
+template <bool RT_ROWS>
+struct SingleMatrixSpan : SingleMatrix {
+    static constexpr int TPW = 2;  // > 1: the kernel runs its multi-tile loop
+    int tiles, per, rows = 0;
+    int nt = 1;
     template <typename ST>
     __device__ __forceinline__ bool select(int bid, const uint4*& wt, const ST*& sc, int& t, int& mrows) {
-        t = bid;
-        mrows = rows;
+        t = bid * per;
+        nt = min(per, tiles - t);
+        if constexpr (RT_ROWS) mrows = rows;
         return true;
     }
+    __device__ __forceinline__ int tiles_here() const { return nt; }
 };
 
 // Scale access: f16 scales of the items (gq, gq+4) share one 16-byte record,

@@ -27,7 +27,7 @@ def _ref_q4(nib, sc, rows, cols, x_f64):
 
 
 @pytest.mark.parametrize("rows,cols", [(11008, 4096), (4096, 11008), (16, 128), (37, 200), (5, 3)])
-@pytest.mark.parametrize("m", [1, 2, 4, 6, 8])  # 5..8 rows: the 8-row tile with live-row masking
+@pytest.mark.parametrize("m", [1, 2, 4, 6, 8, 11, 16])  # 5..16 rows: 8/16-row blocks with live-row masking
 def test_q4_gemv_bf16_activations(dev, rows, cols, m):
     print(f"q4 gemv bf16 rows={rows} cols={cols} m={m}", flush=True)
     nib, sc16, sc = _q4_case(rows, cols, 11 + rows + m)
@@ -42,7 +42,7 @@ def test_q4_gemv_bf16_activations(dev, rows, cols, m):
 
 
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (300, 520)])
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 6, 8])
 def test_q4_gemv_f32_activations(dev, rows, cols, m):
     print(f"q4 gemv f32 rows={rows} cols={cols} m={m}", flush=True)
     nib, sc16, sc = _q4_case(rows, cols, 5 + m)
@@ -69,9 +69,11 @@ def test_q4_gemm_mfma(dev, m):
     assert err < TOL_BF16
 
 
-@pytest.mark.parametrize("m", [8, 16])
-def test_q4_config2_batched(dev, m):
-    rows, cols = 11008, 4096
+@pytest.mark.parametrize("rows,cols,m", [(11008, 4096, 8), (11008, 4096, 16), (11008, 4096, 13),
+                                         (4096, 11008, 7), (4096, 11008, 12)])
+def test_q4_config2_batched(dev, rows, cols, m):
+    """Multi-tile workgroups over the config-2 shape; K=11008 with 8+ rows
+    overflows the LDS staging and takes the MFMA GEMM instead."""
     nib, sc16, sc = _q4_case(rows, cols, 2)
     w = dev.q4_upload_packed(nib, sc16, rows, cols, capi.F16)
     xb = capi.synth_normal(20 + m, m * cols, 1.0, capi.BF16)
