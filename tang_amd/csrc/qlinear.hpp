@@ -349,7 +349,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         wt = wsel;
         sc = ssel;
     }
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave index in a scalar register: item indices, validity tests and the
+    // wave's weight / scale addresses then run on the scalar unit
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r = lane & 15;
     const int nmine = (GQ - wave + NW - 1) / NW;  // items of this wave (wave-uniform)
 
@@ -413,12 +415,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         }
     }
     // 2. weights and scales in flight
+    //    Issue order = consumption order (a record before the weights of its
+    //    items): loads complete in order, so an item never waits for a load
+    //    issued after its own.
     uint4 wbuf[D];
-    typename SR::Rec sbuf[NS];
+    typename SR::Rec sbuf[NS], scur;
 #pragma unroll
-    for (int u = 0; u < D; u++) wbuf[u] = ldg_stream(wp + (size_t)item_gq(u) * 64);
-#pragma unroll
-    for (int v = 0; v < NS; v++) sbuf[v] = *scale_ptr(v * SI);
+    for (int u = 0; u < D; u++) {
+        if (u % SI == 0) sbuf[u / SI] = *scale_ptr(u);
+        wbuf[u] = ldg_stream(wp + (size_t)item_gq(u) * 64);
+    }
     float inv_rms = 1.0f;
     if (NORM) {
         float part = 0.0f;
@@ -498,8 +504,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         for (int e = mr_live; e < BS; e++) bw[ij * BS + e] = 0.0f;
 #pragma unroll
     for (int pp = 0; pp < PRE; pp++) {
+        // no wave-uniform skip of whole passes: a load left unconsumed on one
+        // path makes the compiler wait for every outstanding load (weights
+        // included) where the paths join
         const int ci = lane + pp * 64;
-        if (pp * 64 < nchunk) stage(ci < nchunk ? ci : 0, ci < nchunk, xa[pp], xb[pp], nw[pp]);  // wave-uniform test
+        stage(ci < nchunk ? ci : 0, ci < nchunk, xa[pp], xb[pp], nw[pp]);
     }
     for (int base = PRE * 64; base < nchunk; base += BATCH * 64) {  // wave-uniform loop
         // every load of the round first, then the staging (one latency per round)
@@ -519,12 +528,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
         for (int pp = 0; pp < BATCH; pp++) {
             const int ci = base + pp * 64 + lane;
-            if (base + pp * 64 < nchunk) stage(ci < nchunk ? ci : 0, ci < nchunk, ra[pp], rb[pp], rw[pp]);  // wave-uniform
+            stage(ci < nchunk ? ci : 0, ci < nchunk, ra[pp], rb[pp], rw[pp]);
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 
     constexpr int ACC = MR < 4 ? MR : 4;
     // A rows >= MR and C rows >= MR only feed D rows that are discarded, so
@@ -533,40 +542,46 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     const float* cbase = bw + 4 * (q & (BS / 4 - 1));
     for (int tt = 0; tt < ntl; tt++) {  // one trip unless the source groups tiles
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float4_t dprev = {0.0f, 0.0f, 0.0f, 0.0f};
-    float sprev = 0.0f;
 
     auto step = [&](auto refill_tag, int u, int i) {
-        const bool valid = i < nmine;
-        const int ii = valid ? i : 0;
         const uint4 wv = wbuf[u];
-        const typename SR::Rec sv = sbuf[u / SI];
+        if (u % SI == 0) scur = sbuf[u / SI];  // this record serves items i .. i+SI-1
+        const typename SR::Rec sv = scur;
+        if constexpr (decltype(refill_tag)::value) {
+            if (u % SI == 0) sbuf[u / SI] = *scale_ptr(i + D);
+            wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
+        }
+        if (i >= nmine) return;  // past this wave's items (wave-uniform: a scalar branch)
         float sj[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) sj[j] = valid ? SR::get(sv, u % SI, j) : 0.0f;
-        if constexpr (decltype(refill_tag)::value) {
-            wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
-            if (u % SI == SI - 1) sbuf[u / SI] = *scale_ptr(i + D - (SI - 1));
-        }
+        for (int j = 0; j < 4; j++) sj[j] = SR::get(sv, u % SI, j);
         const uint32_t wj[4] = {wv.x, wv.y, wv.z, wv.w};
-        const uint4* ai = abase + (size_t)ii * 4 * MR * 4;
-        const float* ci = cbase + ii * 4 * BS;
+        const uint4* ai = abase + (size_t)i * 4 * MR * 4;
+        const float* ci = cbase + i * 4 * BS;
+        // the four groups' LDS operands are read together and their MFMAs
+        // are independent (the bias rides in C), so one LDS latency and one
+        // MFMA latency cover the item; only the scale FMAs are ordered
+        uint4 aq[4];
+        float4 cb[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            aq[j] = ai[j * MR * 4];
+            cb[j] = *(const float4*)(ci + j * BS);
+        }
+        float4_t d[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             uint32_t p[4];
             nib_pairs_perm(wj[j], p);
             const uint4 bq = make_uint4(p[0], p[1], p[2], p[3]);
-            const uint4 aq = ai[j * MR * 4];
-            const float4 cb = *(const float4*)(ci + j * BS);
-            const float4_t c = {cb.x, cb.y, cb.z, cb.w};
-            const float4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8_t, aq), __builtin_bit_cast(bf16x8_t, bq), c, 0, 0, 0);
-            // software pipeline: scale the previous group while this MFMA runs
+            const float4_t c = {cb[j].x, cb[j].y, cb[j].z, cb[j].w};
+            d[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, aq[j]),
+                                                           __builtin_bit_cast(bf16x8_t, bq), c, 0, 0, 0);
+        }
 #pragma unroll
-            for (int e = 0; e < ACC; e++) acc[e] = __builtin_fmaf(sprev, dprev[e], acc[e]);
-            dprev = d;
-            sprev = sj[j];
-            __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int e = 0; e < ACC; e++) acc[e] = __builtin_fmaf(sj[j], d[j][e], acc[e]);
         }
     };
     const int nbatch = (nmine + D - 1) / D;
@@ -578,17 +593,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
         for (int u = 0; u < D; u++) step(std::false_type{}, u, (nbatch - 1) * D + u);
     }
-#pragma unroll
-    for (int e = 0; e < ACC; e++) acc[e] = __builtin_fmaf(sprev, dprev[e], acc[e]);
     if constexpr (Src::TPW > 1) {
         // the next tile's first items stream in during this tile's reduction;
         // branch-free: the last tile re-reads its own first items (cache hits)
         const int tn = tt + 1 < ntl ? t + 1 : t;
         const uint4* wpn = wt + (size_t)tn * GQ * 64 + lane;
 #pragma unroll
-        for (int u = 0; u < D; u++) wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
-#pragma unroll
-        for (int vv = 0; vv < NS; vv++) sbuf[vv] = *scale_ptr_t(vv * SI, tn);
+        for (int u = 0; u < D; u++) {
+            if (u % SI == 0) sbuf[u / SI] = *scale_ptr_t(u, tn);
+            wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
+        }
     }
 
     // lane (q, r) holds D rows 4q..4q+3 of column r
