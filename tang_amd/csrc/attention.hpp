@@ -182,7 +182,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     __shared__ float vacc[KPB][D + 1];
     __shared__ int s_last;
     const int h = blockIdx.x, s = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int slot = tid / LPK, e = tid % LPK;
     const int kv_dim = n_kv_heads * D;
     const int kv_h = h / (n_heads / n_kv_heads);

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
     constexpr int MLA_PS = MLA_CHUNK + 1;                       // odd stride: the 16 heads in different banks
     __shared__ float m_run[MLA_H], l_run[MLA_H], resc[MLA_H];
     const int b = blockIdx.x, s = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r = lane & 15;
     const int p0 = s * MLA_SPLIT;
     const int len = min(MLA_SPLIT, L - p0);  // >= 1: the grid has ceil(L / MLA_SPLIT) splits

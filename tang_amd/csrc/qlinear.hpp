@@ -869,7 +869,10 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
         sc = ssel;
     }
     const int GQ = Kp >> 7;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // a scalar wave index pays off for the grouped (MoE) source and costs
+    // the dense GEMM ~10% at M=2048 (measured), so only grouped launches use it
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = Src::GROUPED ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int q = lane >> 4, r = lane & 15;
     const int tile0 = (blockIdx.x * 4 + wave) * RT;  // first 16-row tile of this wave
     const int NT = (N + 15) >> 4;
