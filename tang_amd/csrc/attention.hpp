@@ -139,8 +139,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
     // stage every split record into LDS: independent loads, one latency round
     extern __shared__ float recl[];  // [n_splits][D + 2]
     const int total = n_splits * (D + 2);
-#pragma unroll 16
-    for (int i = tid; i < total; i += 256) recl[i] = ld_coherent(&recs[i]);
+    ld_coherent_to_lds(recs, total, recl, tid);
     __syncthreads();
     float mloc = -INFINITY;
     for (int i = tid; i < n_splits; i += 256) mloc = fmaxf(mloc, recl[(size_t)i * (D + 2)]);
@@ -165,9 +164,13 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
 }
 
 // Decode attention (one query, f16 cache), as attn_split_kernel with a single
-// chunk of SPL positions per workgroup: every K and V row of the split is
-// loaded in one round (raw 16-byte pieces, converted at use), then scores,
-// one softmax pass and P.V; records and the last-arrival merge as above.
+// chunk of at most SPL positions per workgroup: every K and V row of the
+// split is loaded in one round (raw 16-byte pieces, converted at use), then
+// scores, one softmax pass and P.V; records and the last-arrival merge as
+// above.  The attended length is read on the device (the launch is replayed
+// for every position); splits past it only write an empty record.  (Sharing
+// the length evenly over all n_splits workgroups was measured slower: more
+// workgroups each paying the record and merge overhead.)
 template <int D, int SPL, bool OUT_BF16>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                           const _Float16* __restrict__ vc, int n_heads, int n_kv_heads,
@@ -186,7 +189,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     const int slot = tid / LPK, e = tid % LPK;
     const int kv_dim = n_kv_heads * D;
     const int kv_h = h / (n_heads / n_kv_heads);
-    const int attend = *cache_start_dev + 1;
+    const int attend = *cache_start_dev + 1;  // <= n_splits * SPL (checked by the host)
     const int j0 = s * SPL;
     const int len = max(0, min(SPL, attend - j0));
     float* recs = part + (size_t)h * n_splits * (D + 2);
@@ -194,18 +197,28 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     if (len == 0) {
         for (int i = tid; i < D + 2; i += 256) st_coherent(&rec[i], i == 0 ? -INFINITY : 0.0f);
     } else {
-        uint4 kr[KPT], vr[KPT];
-#pragma unroll
-        for (int k = 0; k < KPT; k++) {
-            const int row = j0 + min(slot + k * KPB, len - 1);  // clamped: masked below
-            kr[k] = *(const uint4*)(kc + (size_t)row * kv_dim + kv_h * D + e * 8);
-            vr[k] = *(const uint4*)(vc + (size_t)row * kv_dim + kv_h * D + e * 8);
-        }
+        // Issue order = use order (loads complete in order): q, every K row,
+        // then every V row, so the scores start while V is still streaming.
         float qv[8];
         {
             const float4 a = *(const float4*)(q + (size_t)h * D + e * 8);
             const float4 b = *(const float4*)(q + (size_t)h * D + e * 8 + 4);
             qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w; qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+        }
+        // Rows past the split re-read the last row (clamped: no branch around
+        // the loads, which would make the first use wait for all of them;
+        // masked below).  Buffer loads with an out-of-range resource instead
+        // of the clamp measured slower.
+        uint4 kr[KPT], vr[KPT];
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const int row = j0 + min(slot + k * KPB, len - 1);
+            kr[k] = *(const uint4*)(kc + (size_t)row * kv_dim + kv_h * D + e * 8);
+        }
+#pragma unroll
+        for (int k = 0; k < KPT; k++) {
+            const int row = j0 + min(slot + k * KPB, len - 1);
+            vr[k] = *(const uint4*)(vc + (size_t)row * kv_dim + kv_h * D + e * 8);
         }
         const float scale = 1.0f / sqrtf((float)D);
         float sc[KPT];
@@ -266,8 +279,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     extern __shared__ float recl[];  // [n_splits][D + 2]
     __shared__ float redm[256];
     const int total = n_splits * (D + 2);
-#pragma unroll 16
-    for (int i = tid; i < total; i += 256) recl[i] = ld_coherent(&recs[i]);
+    ld_coherent_to_lds(recs, total, recl, tid);
     __syncthreads();
     float mloc = -INFINITY;
     for (int i = tid; i < n_splits; i += 256) mloc = fmaxf(mloc, recl[(size_t)i * (D + 2)]);

@@ -38,6 +38,33 @@ __device__ __forceinline__ int ld_coherent(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Cache-policy bit of a gfx950 vector memory access that makes it coherent
+// across XCDs (the bit the relaxed agent-scope atomics above carry).
+constexpr int CPOL_SC1 = 16;
+// dword 3 of a raw (untyped) buffer resource.
+constexpr int BUFFER_RSRC_W3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, BUFFER_RSRC_W3);
+}
+
+// Copy n floats that other workgroups stored with st_coherent into LDS.
+// Same coherence as ld_coherent, but plain buffer loads, which the compiler
+// does not serialise (atomic loads each wait for the previous one): sixteen
+// per thread are in flight per round.  Call with the whole 256-thread block.
+__device__ __forceinline__ void ld_coherent_to_lds(const float* src, int n, float* dst, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(src, (uint32_t)n * 4u);
+    for (int base = 0; base < n; base += 16 * 256) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++)  // past n: out of the resource, reads 0
+            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (base + tid + u * 256) * 4, 0, CPOL_SC1));
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (base + tid + u * 256 < n) dst[base + tid + u * 256] = v[u];
+    }
+}
 // Count this workgroup's arrival; true in the last of `total` to arrive
 // (which also resets the counter).  Call with the whole block after every
 // thread's st_coherent stores.
