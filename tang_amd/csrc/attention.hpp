@@ -163,6 +163,198 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
     }
 }
 
+// Causal prefill attention on MFMA (f16 cache, bf16 output), flash style:
+// one workgroup = 64 consecutive queries of one head, each wave 16 of them;
+// key blocks of 64 stream through LDS (K row-major, V transposed), with
+// online softmax in registers.  Both products run transposed so that no
+// operand needs a cross-lane shuffle:
+//   S^T = K . Q^T   (A = K rows from LDS, B = the wave's queries, kept in
+//                    registers as f16, pre-scaled by 1/sqrt(D)); lane (g, r)
+//                    then holds the scores of query r for keys 4g..4g+3 of
+//                    each 16-key tile;
+//   O^T += V^T . P^T (A = V^T rows from LDS, B = those scores as f16); the
+//                    MFMA's k index j of lane group g stands for key 4g+j of
+//                    the first tile of a 32-key chunk (j < 4) or 4g+j-4 of
+//                    the second, the same order in A and B; lane (g, r)
+//                    accumulates dims 4g..4g+3 of each 16-dim tile for query r,
+//                    so the softmax rescale uses the lane's own query.
+// Query i (0 <= i < n) sits at position pos0 + i and attends keys
+// 0..pos0+i (kv_attention, cpu.rs:257-315).  K/V rows are read clamped to the
+// last valid key so masked lanes only ever see finite values.
+typedef _Float16 attn_f16x8_t __attribute__((ext_vector_type(8)));
+typedef float attn_f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t attn_u32x4_t __attribute__((ext_vector_type(4)));  // (uint4 arrays captured by the
+                                                                    // staging lambdas went to scratch)
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ q, int ldq,
+                                                           const _Float16* __restrict__ kc,
+                                                           const _Float16* __restrict__ vc, int n_heads,
+                                                           int n_kv_heads, int pos0, int n,
+                                                           uint16_t* __restrict__ out, int ldo) {
+    constexpr int KB = 64;          // keys per block
+    constexpr int KS = D + 8;       // Ks row stride (halves)
+    constexpr int VS = KB + 8;      // Vt row stride (halves)
+    constexpr int NDC = D / 32;     // 32-dim k-steps of S
+    constexpr int NDT = D / 16;     // 16-dim tiles of O
+    constexpr int CPR = D / 8;      // 16-byte chunks per K/V row
+    constexpr int KLD = KB * CPR / 256;        // K chunks per thread per block
+    constexpr int VLD = (KB / 2) * CPR / 256;  // V chunk pairs per thread per block
+    static_assert(KLD >= 1 && VLD >= 1 && NDC >= 1, "head_dim must be 64 or 128");
+    __shared__ __align__(16) _Float16 Ks[KB * KS];
+    __shared__ __align__(16) _Float16 Vt[D * VS];
+    const int h = blockIdx.y, kv_h = h / (n_heads / n_kv_heads), kv_dim = n_kv_heads * D;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, r = lane & 15;
+    const int qi = blockIdx.x * 64 + wave * 16 + r;  // this lane's query
+    const int qpos = pos0 + qi;
+    const int last_key = pos0 + n - 1;
+    const float scale = 1.0f / sqrtf((float)D);
+
+    attn_f16x8_t qb[NDC];
+    {
+        const float* qp = q + (size_t)min(qi, n - 1) * ldq + h * D + 8 * g;
+#pragma unroll
+        for (int dc = 0; dc < NDC; dc++) {
+            const float4 a = *(const float4*)(qp + dc * 32);
+            const float4 b = *(const float4*)(qp + dc * 32 + 4);
+            qb[dc] = attn_f16x8_t{(_Float16)(a.x * scale), (_Float16)(a.y * scale), (_Float16)(a.z * scale),
+                                  (_Float16)(a.w * scale), (_Float16)(b.x * scale), (_Float16)(b.y * scale),
+                                  (_Float16)(b.z * scale), (_Float16)(b.w * scale)};
+        }
+    }
+    attn_f32x4_t o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) o[dt] = attn_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int qlast = min((int)blockIdx.x * 64 + 63, n - 1);
+    const int nkb = (pos0 + qlast) / KB + 1;
+
+    attn_u32x4_t kr[KLD], vr[VLD][2];
+    auto gload = [&](int kb) {
+        const int key0 = kb * KB;
+#pragma unroll
+        for (int p = 0; p < KLD; p++) {
+            const int idx = tid + 256 * p, key = idx / CPR, c = idx % CPR;
+            const size_t row = (size_t)min(key0 + key, last_key);
+            kr[p] = *(const attn_u32x4_t*)(kc + row * kv_dim + kv_h * D + c * 8);
+        }
+#pragma unroll
+        for (int p = 0; p < VLD; p++) {
+            const int idx = tid + 256 * p, c = idx % CPR, kk = idx / CPR;
+            const size_t r0 = (size_t)min(key0 + 2 * kk, last_key), r1 = (size_t)min(key0 + 2 * kk + 1, last_key);
+            vr[p][0] = *(const attn_u32x4_t*)(vc + r0 * kv_dim + kv_h * D + c * 8);
+            vr[p][1] = *(const attn_u32x4_t*)(vc + r1 * kv_dim + kv_h * D + c * 8);
+        }
+    };
+    // Vt column swizzle: XOR of the key index's bits 2-4 with the dim's bits
+    // 3-5 keeps 4-key groups contiguous and spreads the transposing writes
+    // over the banks.
+    auto vcol = [](int dim, int key) { return key ^ (((dim >> 3) & 7) << 2); };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int p = 0; p < KLD; p++) {
+            const int idx = tid + 256 * p, key = idx / CPR, c = idx % CPR;
+            *(attn_u32x4_t*)&Ks[key * KS + c * 8] = kr[p];
+        }
+#pragma unroll
+        for (int p = 0; p < VLD; p++) {
+            const int idx = tid + 256 * p, c = idx % CPR, kk = idx / CPR;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int dim = c * 8 + i;
+                const uint32_t wa = vr[p][0][i >> 1], wb = vr[p][1][i >> 1];
+                const uint32_t lo = (i & 1) ? (wa >> 16) : (wa & 0xFFFFu);
+                const uint32_t hi = (i & 1) ? (wb >> 16) : (wb & 0xFFFFu);
+                *(uint32_t*)&Vt[dim * VS + vcol(dim, 2 * kk)] = lo | (hi << 16);
+            }
+        }
+    };
+
+    gload(0);
+    for (int kb = 0; kb < nkb; kb++) {
+        __syncthreads();  // the previous block's LDS reads are done
+        lstore();
+        __syncthreads();
+        if (kb + 1 < nkb) gload(kb + 1);  // next block in flight during this one's math
+        attn_f32x4_t sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            sc[kt] = attn_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int dc = 0; dc < NDC; dc++) {
+                const attn_f16x8_t a = *(const attn_f16x8_t*)&Ks[(kt * 16 + r) * KS + dc * 32 + 8 * g];
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[dc], sc[kt], 0, 0, 0);
+            }
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = kb * KB + kt * 16 + 4 * g + i;
+                if (key > qpos) sc[kt][i] = -INFINITY;
+                bm = fmaxf(bm, sc[kt][i]);
+            }
+        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const float mn = fmaxf(m_run, bm);  // finite: key 0 is in block 0 for every query
+        const float alpha = expf(m_run - mn);
+        float ps = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float p = expf(sc[kt][i] - mn);
+                sc[kt][i] = p;
+                ps += p;
+            }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        l_run = l_run * alpha + ps;
+        m_run = mn;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) o[dt] *= alpha;
+#pragma unroll
+        for (int kc2 = 0; kc2 < 2; kc2++) {
+            const attn_f16x8_t pb = {(_Float16)sc[2 * kc2][0], (_Float16)sc[2 * kc2][1], (_Float16)sc[2 * kc2][2],
+                                     (_Float16)sc[2 * kc2][3], (_Float16)sc[2 * kc2 + 1][0],
+                                     (_Float16)sc[2 * kc2 + 1][1], (_Float16)sc[2 * kc2 + 1][2],
+                                     (_Float16)sc[2 * kc2 + 1][3]};
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                const int dim = dt * 16 + r, c0 = kc2 * 32 + 4 * g;
+                const uint2 lo = *(const uint2*)&Vt[dim * VS + vcol(dim, c0)];
+                const uint2 hi = *(const uint2*)&Vt[dim * VS + vcol(dim, c0 + 16)];
+                const attn_f16x8_t a = __builtin_bit_cast(attn_f16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[dt], 0, 0, 0);
+            }
+        }
+    }
+    if (qi < n) {
+        const float inv = 1.0f / l_run;
+        uint16_t* op = out + (size_t)qi * ldo + h * D + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const uint32_t w0 = f32_to_bf16_rne(o[dt][0] * inv) | ((uint32_t)f32_to_bf16_rne(o[dt][1] * inv) << 16);
+            const uint32_t w1 = f32_to_bf16_rne(o[dt][2] * inv) | ((uint32_t)f32_to_bf16_rne(o[dt][3] * inv) << 16);
+            *(uint2*)(op + dt * 16) = make_uint2(w0, w1);
+        }
+    }
+}
+
+inline void launch_attn_prefill(const float* q, int ldq, const _Float16* kc, const _Float16* vc, int n_heads,
+                                int n_kv_heads, int head_dim, int pos0, int n, uint16_t* out, int ldo, hipStream_t s) {
+    TH_REQUIRE(n >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0, "prefill attention: bad shape");
+    const dim3 grid((unsigned)ceil_div((size_t)n, (size_t)64), (unsigned)n_heads);
+    switch (head_dim) {
+        case 64: hipLaunchKernelGGL((attn_prefill_kernel<64>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
+        case 128: hipLaunchKernelGGL((attn_prefill_kernel<128>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
+        default: throw Error(TH_ERR_INVALID, "prefill attention: head_dim must be 64 or 128");
+    }
+    TH_LAUNCH_CHECK();
+}
+
 // Decode attention (one query, f16 cache), as attn_split_kernel with a single
 // chunk of at most SPL positions per workgroup: every K and V row of the
 // split is loaded in one round (raw 16-byte pieces, converted at use), then

@@ -472,10 +472,15 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
         hipLaunchKernelGGL(prefill_rope_kv_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_qkv, (int)pos0,
                            m->rope_cos, m->rope_sin, m->qd, m->kvd, hd, m->pf_q, kc, vc);
         TH_LAUNCH_CHECK();
-        float* part = (float*)device_scratch(dev, n * c.n_heads * n_splits * (hd + 2) * sizeof(float));
-        int* counters = device_counters(dev, n * c.n_heads);
-        launch_attn_split<true>(m->pf_q, kc, vc, true, (int)pos0, (int)n, c.n_heads, c.n_kv_heads, hd, subs, n_splits,
-                                part, counters, (void*)m->pf_att, nullptr, s);
+        if (hd == 64 || hd == 128) {  // causal flash attention on MFMA
+            launch_attn_prefill(m->pf_q, m->qd, kc, vc, c.n_heads, c.n_kv_heads, hd, (int)pos0, (int)n,
+                                (uint16_t*)m->pf_att, m->qd, s);
+        } else {
+            float* part = (float*)device_scratch(dev, n * c.n_heads * n_splits * (hd + 2) * sizeof(float));
+            int* counters = device_counters(dev, n * c.n_heads);
+            launch_attn_split<true>(m->pf_q, kc, vc, true, (int)pos0, (int)n, c.n_heads, c.n_kv_heads, hd, subs,
+                                    n_splits, part, counters, (void*)m->pf_att, nullptr, s);
+        }
         launch_q4_linear(m->wo[l], m->pf_att, TH_BF16, n, m->qd, m->pf_y, d, s, dev);
         hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
         TH_LAUNCH_CHECK();
