@@ -36,6 +36,9 @@ const th_sampling_config& sampler_config(const th_sampler* s);
 // Zero-initialised ints that kernels leave zero again on exit (arrival
 // counters of the last-workgroup merges); grow-only.
 int* device_counters(th_device* dev, size_t n);
+// Second stream-ordered workspace, used for activations converted once per
+// GEMM call (may be held at the same time as device_scratch).
+void* device_scratch_x(th_device* dev, size_t bytes);
 void require_len(const th_buffer* b, th_dtype dt, size_t n, const char* what);
 void require_len_any(const th_buffer* b, size_t n, const char* what);
 

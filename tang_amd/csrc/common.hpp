@@ -79,6 +79,8 @@ struct th_device {
     int num_cus = 0;
     void* scratch = nullptr;  // stream-ordered workspace (split-K and attention partials)
     size_t scratch_bytes = 0;
+    void* scratch_x = nullptr;  // stream-ordered workspace for GEMM operands prepared in f16
+    size_t scratch_x_bytes = 0;
     int* counters = nullptr;  // see device_counters
     size_t n_counters = 0;
 };

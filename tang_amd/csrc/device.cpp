@@ -30,6 +30,20 @@ void* device_scratch(th_device* dev, size_t bytes) {
     return dev->scratch;
 }
 
+void* device_scratch_x(th_device* dev, size_t bytes) {
+    if (bytes <= dev->scratch_x_bytes) return dev->scratch_x;
+    if (dev->scratch_x) {
+        TH_HIP(hipStreamSynchronize(dev->stream));
+        TH_HIP(hipFree(dev->scratch_x));
+        dev->scratch_x = nullptr;
+        dev->scratch_x_bytes = 0;
+    }
+    size_t want = std::max(bytes, (size_t)1 << 20);
+    TH_HIP(hipMalloc(&dev->scratch_x, want));
+    dev->scratch_x_bytes = want;
+    return dev->scratch_x;
+}
+
 int* device_counters(th_device* dev, size_t n) {
     if (n <= dev->n_counters) return dev->counters;
     if (dev->counters) {
@@ -221,6 +235,7 @@ int th_device_destroy(th_device* d) {
     (void)hipSetDevice(d->ordinal);
     (void)hipStreamSynchronize(d->stream);
     if (d->scratch) (void)hipFree(d->scratch);
+    if (d->scratch_x) (void)hipFree(d->scratch_x);
     if (d->counters) (void)hipFree(d->counters);
     (void)hipEventDestroy(d->ev_start);
     (void)hipEventDestroy(d->ev_stop);

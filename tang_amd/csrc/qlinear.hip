@@ -125,9 +125,19 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __re
     }
 }
 
-template <int RT, int CB, bool XF32, typename ST>
+template <int RT, int CB, bool XF32, typename ST, bool XP = false>
 static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
                            hipStream_t s, th_device* dev) {
+    if constexpr (XP) {  // convert the activations once instead of in every column block
+        const size_t total = m * (w->Kp / 8);
+        uint4* xp = (uint4*)device_scratch_x(dev, total * sizeof(uint4));
+        const unsigned blocks = (unsigned)std::min<size_t>(ceil_div(total, 256), 4096);
+        hipLaunchKernelGGL((q4_gemm_xprep_kernel<XF32>), dim3(blocks), dim3(256), 0, s, x, (int)ldx, (int)w->cols,
+                           (int)w->Kp, (int)m, xp);
+        TH_LAUNCH_CHECK();
+        x = xp;
+        ldx = w->Kp;
+    }
     const size_t NT = w->Np / 16, GQ = w->Kp / 128;
     const unsigned gx = (unsigned)ceil_div(NT, 4 * RT);
     const unsigned gy = (unsigned)ceil_div(m, 16 * CB);
@@ -146,7 +156,8 @@ static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t 
     GemmDense src;
     src.M = (int)m;
     EpiGemmStore epi{out, ldo, (size_t)m * (size_t)ldo};
-    hipLaunchKernelGGL((q4_gemm_mfma_kernel<RT, CB, XF32, ST>), dim3(gx, gy, (unsigned)ks), dim3(256), 0, s,
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<RT, CB, XF32 && !XP, ST, GemmDense, EpiGemmStore, XP>),
+                       dim3(gx, gy, (unsigned)ks), dim3(256), 0, s,
                        (const uint4*)w->data, (const ST*)w->scales, x, epi, src, (int)w->rows, (int)w->cols,
                        (int)w->Kp, (int)ldx, gps);
     TH_LAUNCH_CHECK();
@@ -170,7 +181,10 @@ static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx
     else if (!XF32 && m <= 8 && fits8) q4_span_launch<8, false, ST>(w, x, m, ldx, y, ldy, s, cus);
     else if (!XF32 && m <= 16 && fits16) q4_span_launch<16, false, ST>(w, x, m, ldx, y, ldy, s, cus);
     else if (m <= 16) q4_mfma_launch<1, 1, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
-    else q4_mfma_launch<2, 4, XF32, ST>(w, x, m, ldx, y, ldy, s, dev);
+    // activations converted to f16 once per call; 64-row column blocks up to
+    // M=1024, 128-row blocks beyond (measured best of 2x4, 1x8, 2x6, 2x8, 4x4, 4x8)
+    else if (m <= 1024) q4_mfma_launch<2, 4, XF32, ST, true>(w, x, m, ldx, y, ldy, s, dev);
+    else q4_mfma_launch<2, 8, XF32, ST, true>(w, x, m, ldx, y, ldy, s, dev);
 }
 
 void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,

@@ -853,7 +853,50 @@ struct EpiGemmStore {
     }
 };
 
-template <int RT, int CB, bool XF32, typename ST, typename Src = GemmDense, typename Epi = EpiGemmStore>
+// Activations for the MFMA GEMM converted once per call (XP mode): f16 with
+// the rounding the GEMM's own staging applies, each 8-value chunk already in
+// nibble-pair order (x0,x4,x1,x5,x2,x6,x3,x7), rows zero-padded to Kp.
+template <bool XF32>
+__global__ __launch_bounds__(256) void q4_gemm_xprep_kernel(const void* __restrict__ xin, int ldx, int K, int Kp,
+                                                            int M, uint4* __restrict__ out) {
+    const int cpr = Kp >> 3;
+    const size_t total = (size_t)M * cpr;
+    const bool vec = (ldx & 7) == 0 && (((uintptr_t)xin) & 15) == 0;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(i / cpr), k0 = (int)(i % cpr) * 8;
+        float xv[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) xv[e] = 0.0f;
+        if (XF32) {
+            const float* xr = (const float*)xin + (size_t)m * ldx;
+            if (vec && k0 + 8 <= K) {
+                const float4 a = *(const float4*)(xr + k0), b = *(const float4*)(xr + k0 + 4);
+                xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+                xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+            } else {
+                for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = xr[k0 + e];
+            }
+        } else {
+            const uint16_t* xr = (const uint16_t*)xin + (size_t)m * ldx;
+            if (vec && k0 + 8 <= K) {
+                const uint4 a = *(const uint4*)(xr + k0);
+                const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
+                    xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
+                }
+            } else {
+                for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = bf16_bits_to_f32(xr[k0 + e]);
+            }
+        }
+        out[i] = make_uint4(pack_half2(xv[0], xv[4]), pack_half2(xv[1], xv[5]), pack_half2(xv[2], xv[6]),
+                            pack_half2(xv[3], xv[7]));
+    }
+}
+
+template <int RT, int CB, bool XF32, typename ST, typename Src = GemmDense, typename Epi = EpiGemmStore,
+          bool XP = false>
 __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restrict__ wt,
                                                            const ST* __restrict__ sc,
                                                            const void* __restrict__ xin, Epi epi, Src src,
@@ -897,6 +940,11 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
             const int cb = idx >> 8;
             const int ml = cb * 16 + col;
             const int k0 = gq * 128 + j * 32 + qq * 8;
+            if constexpr (XP) {  // prepared: f16, permuted, padded (ldx = Kp)
+                regs[i] = ml < mrows ? *(const uint4*)((const uint16_t*)xin + (size_t)src.x_row(ml) * ldx + k0)
+                                     : make_uint4(0, 0, 0, 0);
+                continue;
+            }
             float xv[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) xv[e] = 0.0f;

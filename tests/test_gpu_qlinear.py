@@ -55,7 +55,7 @@ def test_q4_gemv_f32_activations(dev, rows, cols, m):
     assert err < TOL_F32
 
 
-@pytest.mark.parametrize("m", [9, 16, 40, 64, 130])
+@pytest.mark.parametrize("m", [9, 16, 40, 64, 130, 1100])  # 1100: the 128-row column blocks
 def test_q4_gemm_mfma(dev, m):
     rows, cols = 1000, 1536
     print(f"q4 mfma m={m}", flush=True)
@@ -67,6 +67,19 @@ def test_q4_gemm_mfma(dev, m):
     err = max_abs_rel(y, ref)
     print("max_abs_rel", err)
     assert err < TOL_BF16
+
+
+def test_q4_gemm_mfma_f32_activations(dev):
+    """The GEMM's one-pass activation conversion from f32 (ragged K)."""
+    rows, cols, m = 300, 1000, 70
+    nib, sc16, sc = _q4_case(rows, cols, 8)
+    w = dev.q4_upload_packed(nib, sc16, rows, cols, capi.F16)
+    xf = capi.synth_normal(9, m * cols, 1.0, capi.F32)
+    y = dev.gemm_q4(dev.upload(xf), m, w).to_numpy().reshape(m, rows)
+    ref = _ref_q4(nib, sc, rows, cols, xf.reshape(m, cols).astype(np.float64))
+    err = max_abs_rel(y, ref)
+    print("max_abs_rel", err)
+    assert err < TOL_BF16  # f16-rounded operands, as the bf16 bar
 
 
 @pytest.mark.parametrize("rows,cols,m", [(11008, 4096, 8), (11008, 4096, 16), (11008, 4096, 13),
