@@ -455,14 +455,21 @@ constexpr int MOE_GEMM_CB = 4;  // 16-slot blocks per work item (64 slots)
 
 template <typename Epi>
 static void moe_grouped_gemm(const th_moe* m, const th_qweight* w0, const uint4* const* data,
-                             const _Float16* const* scales, const uint16_t* x, const int* slot_token, size_t max_work,
-                             Epi epi) {
+                             const _Float16* const* scales, const uint16_t* x, size_t x_rows, const int* slot_token,
+                             size_t max_work, Epi epi) {
+    // the x_rows activation rows (tokens, or slots) converted to f16 once
+    const size_t total = x_rows * (w0->Kp / 8);
+    uint4* xp = (uint4*)device_scratch_x(m->dev, total * sizeof(uint4));
+    hipLaunchKernelGGL((q4_gemm_xprep_kernel<false>), dim3((unsigned)std::min<size_t>(ceil_div(total, 256), 4096)),
+                       dim3(256), 0, m->dev->stream, (const void*)x, (int)w0->cols, (int)w0->cols, (int)w0->Kp,
+                       (int)x_rows, xp);
+    TH_LAUNCH_CHECK();
     MoeGemmSrc src{m->work, data, scales, slot_token};
     const unsigned gx = (unsigned)ceil_div(w0->Np / 16, (size_t)(4 * MOE_GEMM_RT));
-    hipLaunchKernelGGL((q4_gemm_mfma_kernel<MOE_GEMM_RT, MOE_GEMM_CB, false, _Float16, MoeGemmSrc, Epi>),
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<MOE_GEMM_RT, MOE_GEMM_CB, false, _Float16, MoeGemmSrc, Epi, true>),
                        dim3(gx, (unsigned)max_work, 1), dim3(256), 0, m->dev->stream, (const uint4*)nullptr,
-                       (const _Float16*)nullptr, (const void*)x, epi, src, (int)w0->rows, (int)w0->cols,
-                       (int)w0->Kp, (int)w0->cols, (int)(w0->Kp / 128));
+                       (const _Float16*)nullptr, (const void*)xp, epi, src, (int)w0->rows, (int)w0->cols,
+                       (int)w0->Kp, (int)w0->Kp, (int)(w0->Kp / 128));
     TH_LAUNCH_CHECK();
 }
 
@@ -563,9 +570,9 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
         moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeStore, 4>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr,
                                                        max_work, EpiMoeStore{{}, m->ybuf, (int)m->d});
     } else {
-        moe_grouped_gemm(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token, max_work,
+        moe_grouped_gemm(m, m->gu[0], m->gu_data, m->gu_scales, hx, T, m->slot_token, max_work,
                          EpiGemmMoeSwiGLU{m->hbuf, (int)m->ff});
-        moe_grouped_gemm(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr, max_work,
+        moe_grouped_gemm(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, T * (m->k + m->S), nullptr, max_work,
                          EpiGemmMoeStore{m->ybuf, (int)m->d});
     }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, s, m->ybuf, m->token_slot,
