@@ -186,12 +186,16 @@ __global__ void prefill_embed_kernel(const uint16_t* __restrict__ embed, const i
         x[(size_t)row * d + i] = __uint_as_float((uint32_t)src[i] << 16);
 }
 
-// RMSNorm of one row to the bf16 linear input, with the decode engine's
-// rounding and summation order: per-16-element sums of squares, four per
-// lane, a fixed butterfly, then x * inv_rms * w (cpu.rs:126-149) rounded to
-// bf16 (cuda.rs:22).  One wave per row; d <= 4096.
+// RMSNorm of one row to the linear input, with the decode engine's rounding
+// and summation order: per-16-element sums of squares, four per lane, a fixed
+// butterfly, then x * inv_rms * w (cpu.rs:126-149) rounded to bf16
+// (cuda.rs:22).  One wave per row; d <= 4096, d % 8 == 0.  XP: the value is
+// written as f16 (exact for a bf16 value) in the MFMA GEMM's prepared layout
+// (8-value chunks as x0,x4,x1,x5,x2,x6,x3,x7; rows of ldo >= d, zero past d);
+// otherwise as bf16 rows of ldo.
+template <bool XP>
 __global__ __launch_bounds__(64) void prefill_rmsnorm_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
-                                                            int d, float eps, uint16_t* __restrict__ out) {
+                                                            int d, float eps, uint16_t* __restrict__ out, int ldo) {
     const int row = blockIdx.x, lane = threadIdx.x;
     const float* xr = x + (size_t)row * d;
     float part = 0.0f;
@@ -199,17 +203,49 @@ __global__ __launch_bounds__(64) void prefill_rmsnorm_kernel(const float* __rest
     for (int u = 0; u < 4; u++) {
         const int t = lane + 64 * u;
         float sq = 0.0f;
-        if (t * 16 < d)
-            for (int i = 0; i < 16; i++) {
-                const float v = xr[t * 16 + i];
-                sq += v * v;
+        if (t * 16 < d) {
+            float v[16];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float4 f = *(const float4*)(xr + t * 16 + 4 * c);
+                v[4 * c] = f.x; v[4 * c + 1] = f.y; v[4 * c + 2] = f.z; v[4 * c + 3] = f.w;
             }
+#pragma unroll
+            for (int i = 0; i < 16; i++) sq += v[i] * v[i];
+        }
         part += sq;
     }
     const float tot = wave_sum(part);
     const float inv = 1.0f / sqrtf(tot / (float)d + eps);
-    for (int i = lane; i < d; i += 64)
-        out[(size_t)row * d + i] = f32_to_bf16_rne(xr[i] * inv * __uint_as_float((uint32_t)w[i] << 16));
+    uint16_t* orow = out + (size_t)row * ldo;
+    for (int c = lane; c * 8 < ldo; c += 64) {  // 8-value chunks
+        const int k0 = c * 8;
+        float y[8];
+        if (k0 < d) {
+            const float4 a = *(const float4*)(xr + k0), b = *(const float4*)(xr + k0 + 4);
+            const uint4 wb = *(const uint4*)(w + k0);
+            const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            const uint32_t ww[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t wbits = (i & 1) ? (ww[i >> 1] >> 16) : (ww[i >> 1] & 0xFFFFu);
+                y[i] = bf16_bits_to_f32(f32_to_bf16_rne(xv[i] * inv * __uint_as_float(wbits << 16)));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) y[i] = 0.0f;
+        }
+        if (XP) {
+            *(uint4*)(orow + k0) = make_uint4(pack_half2(y[0], y[4]), pack_half2(y[1], y[5]), pack_half2(y[2], y[6]),
+                                              pack_half2(y[3], y[7]));
+        } else if (k0 < d) {
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                o[i] = (uint32_t)f32_to_bf16_rne(y[2 * i]) | ((uint32_t)f32_to_bf16_rne(y[2 * i + 1]) << 16);
+            *(uint4*)(orow + k0) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
 }
 
 // RoPE of q and k (device.rs:582-610, as EpiQKV) at position pos0 + row; q to
@@ -239,13 +275,30 @@ __global__ void prefill_add_kernel(float* __restrict__ x, const float* __restric
 }
 
 // SwiGLU of the interleaved gate/up rows (tile b: gate 8b..8b+7, up
-// 8b..8b+7) to the bf16 down-projection input [n][ff].
-__global__ void prefill_swiglu_kernel(const float* __restrict__ gu, int ff, uint16_t* __restrict__ out) {
+// 8b..8b+7) to the down-projection input, rounded to bf16: as bf16 rows of
+// ldo, or (XP) in the MFMA GEMM's prepared f16 layout (zero past ff).  One
+// thread per 8-value chunk; ff % 8 == 0.
+template <bool XP>
+__global__ void prefill_swiglu_kernel(const float* __restrict__ gu, int ff, uint16_t* __restrict__ out, int ldo) {
     const int row = blockIdx.y;
     const float* g = gu + (size_t)row * 2 * ff;
-    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < ff; j += gridDim.x * blockDim.x) {
-        const int b = j >> 3, rr = j & 7;
-        out[(size_t)row * ff + j] = f32_to_bf16_rne(swiglu_f64(g[16 * b + rr], g[16 * b + 8 + rr]));
+    uint16_t* orow = out + (size_t)row * ldo;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c * 8 < ldo; c += gridDim.x * blockDim.x) {
+        const int b = c;  // chunk c = tile c's eight gate/up pairs
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            y[i] = c * 8 < ff ? bf16_bits_to_f32(f32_to_bf16_rne(swiglu_f64(g[16 * b + i], g[16 * b + 8 + i]))) : 0.0f;
+        if (XP) {
+            *(uint4*)(orow + c * 8) = make_uint4(pack_half2(y[0], y[4]), pack_half2(y[1], y[5]),
+                                                 pack_half2(y[2], y[6]), pack_half2(y[3], y[7]));
+        } else if (c * 8 < ff) {
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                o[i] = (uint32_t)f32_to_bf16_rne(y[2 * i]) | ((uint32_t)f32_to_bf16_rne(y[2 * i + 1]) << 16);
+            *(uint4*)(orow + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
     }
 }
 
@@ -440,9 +493,9 @@ static void prefill_reserve(th_llama* m, size_t rows) {
     m->pf_qkv = dalloc<float>(rows * (m->qd + 2 * m->kvd));
     m->pf_q = dalloc<float>(rows * m->qd);
     m->pf_gu = dalloc<float>(rows * 2 * ff);
-    m->pf_xb = dalloc<uint16_t>(rows * d);
+    m->pf_xb = dalloc<uint16_t>(rows * round_up(d, 128));  // bf16 rows, or prepared rows of Kp
     m->pf_att = dalloc<uint16_t>(rows * m->qd);
-    m->pf_sg = dalloc<uint16_t>(rows * ff);
+    m->pf_sg = dalloc<uint16_t>(rows * round_up(ff, 128));
     m->pf_tok = dalloc<int32_t>(rows);
     m->pf_rows = rows;
 }
@@ -458,6 +511,22 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
     hipLaunchKernelGGL(prefill_embed_kernel, dim3(4, (unsigned)n), dim3(256), 0, s, m->embed, m->pf_tok, d, m->pf_x);
     TH_LAUNCH_CHECK();
     const size_t cache_layer = (size_t)c.max_seq * m->kvd;
+    // Above 16 rows the linears run on the MFMA GEMM, whose activation layout
+    // the RMSNorm and SwiGLU kernels then write directly.
+    const bool xp = n > 16;
+    auto prefill_norm = [&](const uint16_t* w, const th_qweight* consumer) {
+        if (xp)
+            hipLaunchKernelGGL(prefill_rmsnorm_kernel<true>, dim3((unsigned)n), dim3(64), 0, s, m->pf_x, w, d, c.eps,
+                               m->pf_xb, (int)consumer->Kp);
+        else
+            hipLaunchKernelGGL(prefill_rmsnorm_kernel<false>, dim3((unsigned)n), dim3(64), 0, s, m->pf_x, w, d,
+                               c.eps, m->pf_xb, d);
+        TH_LAUNCH_CHECK();
+    };
+    auto linear = [&](const th_qweight* w, const uint16_t* xin, int k, float* y, int ldy) {
+        if (xp) launch_q4_linear_prepared(w, xin, n, y, ldy, s, dev);
+        else launch_q4_linear(w, xin, TH_BF16, n, k, y, ldy, s, dev);
+    };
     // split attention: few enough splits that q_len * heads * splits records fit the scratch
     const size_t attended = pos0 + n;
     const int subs = (int)std::max<size_t>(1, ceil_div(attended, (size_t)ATTN_SUB * 8));
@@ -465,10 +534,8 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
     for (int l = 0; l < c.n_layers; l++) {
         _Float16* kc = m->kcache + l * cache_layer;
         _Float16* vc = m->vcache + l * cache_layer;
-        hipLaunchKernelGGL(prefill_rmsnorm_kernel, dim3((unsigned)n), dim3(64), 0, s, m->pf_x,
-                           m->attn_norm + (size_t)l * d, d, c.eps, m->pf_xb);
-        TH_LAUNCH_CHECK();
-        launch_q4_linear(m->wqkv[l], m->pf_xb, TH_BF16, n, d, m->pf_qkv, W, s, dev);
+        prefill_norm(m->attn_norm + (size_t)l * d, m->wqkv[l]);
+        linear(m->wqkv[l], m->pf_xb, d, m->pf_qkv, W);
         hipLaunchKernelGGL(prefill_rope_kv_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_qkv, (int)pos0,
                            m->rope_cos, m->rope_sin, m->qd, m->kvd, hd, m->pf_q, kc, vc);
         TH_LAUNCH_CHECK();
@@ -484,13 +551,16 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
         launch_q4_linear(m->wo[l], m->pf_att, TH_BF16, n, m->qd, m->pf_y, d, s, dev);
         hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
         TH_LAUNCH_CHECK();
-        hipLaunchKernelGGL(prefill_rmsnorm_kernel, dim3((unsigned)n), dim3(64), 0, s, m->pf_x,
-                           m->ffn_norm + (size_t)l * d, d, c.eps, m->pf_xb);
+        prefill_norm(m->ffn_norm + (size_t)l * d, m->wgu[l]);
+        linear(m->wgu[l], m->pf_xb, d, m->pf_gu, 2 * ff);
+        if (xp)
+            hipLaunchKernelGGL(prefill_swiglu_kernel<true>, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_gu, ff,
+                               m->pf_sg, (int)m->wd[l]->Kp);
+        else
+            hipLaunchKernelGGL(prefill_swiglu_kernel<false>, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_gu, ff,
+                               m->pf_sg, ff);
         TH_LAUNCH_CHECK();
-        launch_q4_linear(m->wgu[l], m->pf_xb, TH_BF16, n, d, m->pf_gu, 2 * ff, s, dev);
-        hipLaunchKernelGGL(prefill_swiglu_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_gu, ff, m->pf_sg);
-        TH_LAUNCH_CHECK();
-        launch_q4_linear(m->wd[l], m->pf_sg, TH_BF16, n, ff, m->pf_y, d, s, dev);
+        linear(m->wd[l], m->pf_sg, ff, m->pf_y, d);
         hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
         TH_LAUNCH_CHECK();
     }

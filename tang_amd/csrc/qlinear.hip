@@ -127,8 +127,8 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __re
 
 template <int RT, int CB, bool XF32, typename ST, bool XP = false>
 static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
-                           hipStream_t s, th_device* dev) {
-    if constexpr (XP) {  // convert the activations once instead of in every column block
+                           hipStream_t s, th_device* dev, bool prepared = false) {
+    if (XP && !prepared) {  // convert the activations once instead of in every column block
         const size_t total = m * (w->Kp / 8);
         uint4* xp = (uint4*)device_scratch_x(dev, total * sizeof(uint4));
         const unsigned blocks = (unsigned)std::min<size_t>(ceil_div(total, 256), 4096);
@@ -185,6 +185,19 @@ static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx
     // M=1024, 128-row blocks beyond (measured best of 2x4, 1x8, 2x6, 2x8, 4x4, 4x8)
     else if (m <= 1024) q4_mfma_launch<2, 4, XF32, ST, true>(w, x, m, ldx, y, ldy, s, dev);
     else q4_mfma_launch<2, 8, XF32, ST, true>(w, x, m, ldx, y, ldy, s, dev);
+}
+
+void launch_q4_linear_prepared(const th_qweight* w, const uint16_t* xp, size_t m, float* y, size_t ldy,
+                               hipStream_t s, th_device* dev) {
+    TH_REQUIRE(w && w->bits == 4, "not a q4 weight");
+    TH_REQUIRE(m > 16, "prepared activations feed the MFMA GEMM only (m > 16)");
+    if (w->scale_dtype == TH_F16) {
+        if (m <= 1024) q4_mfma_launch<2, 4, false, _Float16, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
+        else q4_mfma_launch<2, 8, false, _Float16, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
+    } else {
+        if (m <= 1024) q4_mfma_launch<2, 4, false, float, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
+        else q4_mfma_launch<2, 8, false, float, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
+    }
 }
 
 void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
