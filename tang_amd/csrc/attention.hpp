@@ -182,11 +182,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict
 // 0..pos0+i (kv_attention, cpu.rs:257-315).  K/V rows are read clamped to the
 // last valid key so masked lanes only ever see finite values.
 typedef _Float16 attn_f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint32_t attn_pack_h2(float a, float b) {  // two f16, a in the low half
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
 typedef float attn_f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t attn_u32x4_t __attribute__((ext_vector_type(4)));  // (uint4 arrays captured by the
                                                                     // staging lambdas went to scratch)
 
-template <int D>
+template <int D, bool XP>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restrict__ q, int ldq,
                                                            const _Float16* __restrict__ kc,
                                                            const _Float16* __restrict__ vc, int n_heads,
@@ -331,8 +334,25 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
             }
         }
     }
-    if (qi < n) {
-        const float inv = 1.0f / l_run;
+    const float inv = 1.0f / l_run;
+    if constexpr (XP) {
+        // the O projection's prepared layout: the 8-dim chunk of lane groups
+        // g (even) and g+1 goes out from the even lane as (x0,x4,x1,x5,...)
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            float y[4], z[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                y[i] = __uint_as_float((uint32_t)f32_to_bf16_rne(o[dt][i] * inv) << 16);
+                z[i] = __shfl_xor(y[i], 16, 64);
+            }
+            if (qi < n && (g & 1) == 0) {
+                uint16_t* op = out + (size_t)qi * ldo + h * D + dt * 16 + 4 * g;
+                *(uint4*)op = make_uint4(attn_pack_h2(y[0], z[0]), attn_pack_h2(y[1], z[1]),
+                                         attn_pack_h2(y[2], z[2]), attn_pack_h2(y[3], z[3]));
+            }
+        }
+    } else if (qi < n) {
         uint16_t* op = out + (size_t)qi * ldo + h * D + 4 * g;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
@@ -343,13 +363,18 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     }
 }
 
+// out: bf16 rows of ldo, or (xp) the MFMA GEMM's prepared f16 layout (rows
+// of ldo >= n_heads * head_dim, which must then be the consumer's Kp).
 inline void launch_attn_prefill(const float* q, int ldq, const _Float16* kc, const _Float16* vc, int n_heads,
-                                int n_kv_heads, int head_dim, int pos0, int n, uint16_t* out, int ldo, hipStream_t s) {
+                                int n_kv_heads, int head_dim, int pos0, int n, uint16_t* out, int ldo, bool xp,
+                                hipStream_t s) {
     TH_REQUIRE(n >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0, "prefill attention: bad shape");
     const dim3 grid((unsigned)ceil_div((size_t)n, (size_t)64), (unsigned)n_heads);
-    switch (head_dim) {
-        case 64: hipLaunchKernelGGL((attn_prefill_kernel<64>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
-        case 128: hipLaunchKernelGGL((attn_prefill_kernel<128>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
+    switch (head_dim * 2 + (xp ? 1 : 0)) {
+        case 128: hipLaunchKernelGGL((attn_prefill_kernel<64, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
+        case 129: hipLaunchKernelGGL((attn_prefill_kernel<64, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
+        case 256: hipLaunchKernelGGL((attn_prefill_kernel<128, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
+        case 257: hipLaunchKernelGGL((attn_prefill_kernel<128, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
         default: throw Error(TH_ERR_INVALID, "prefill attention: head_dim must be 64 or 128");
     }
     TH_LAUNCH_CHECK();

@@ -51,9 +51,10 @@ th_qweight* q8_pack(th_device* dev, const int8_t* q, size_t ldq, const float* sc
 // y: [m][ldy] f32.
 // The MFMA GEMM on activations already in its prepared layout: f16 rows of
 // w->Kp (zero past K), each 8-value chunk ordered x0,x4,x1,x5,x2,x6,x3,x7.
-// For producers that can write that layout directly; m > 16.
+// For producers that can write that layout directly; m > 16.  accumulate:
+// y += x.W^T (a fused residual add) instead of y = x.W^T.
 void launch_q4_linear_prepared(const th_qweight* w, const uint16_t* xp, size_t m, float* y, size_t ldy,
-                               hipStream_t s, th_device* dev);
+                               hipStream_t s, th_device* dev, bool accumulate = false);
 void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
                       size_t ldy, hipStream_t stream, th_device* dev);
 void launch_q8_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,

@@ -494,7 +494,7 @@ static void prefill_reserve(th_llama* m, size_t rows) {
     m->pf_q = dalloc<float>(rows * m->qd);
     m->pf_gu = dalloc<float>(rows * 2 * ff);
     m->pf_xb = dalloc<uint16_t>(rows * round_up(d, 128));  // bf16 rows, or prepared rows of Kp
-    m->pf_att = dalloc<uint16_t>(rows * m->qd);
+    m->pf_att = dalloc<uint16_t>(rows * round_up((size_t)m->qd, 128));
     m->pf_sg = dalloc<uint16_t>(rows * round_up(ff, 128));
     m->pf_tok = dalloc<int32_t>(rows);
     m->pf_rows = rows;
@@ -539,18 +539,23 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
         hipLaunchKernelGGL(prefill_rope_kv_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_qkv, (int)pos0,
                            m->rope_cos, m->rope_sin, m->qd, m->kvd, hd, m->pf_q, kc, vc);
         TH_LAUNCH_CHECK();
+        const bool xp_att = xp && (hd == 64 || hd == 128);
         if (hd == 64 || hd == 128) {  // causal flash attention on MFMA
             launch_attn_prefill(m->pf_q, m->qd, kc, vc, c.n_heads, c.n_kv_heads, hd, (int)pos0, (int)n,
-                                (uint16_t*)m->pf_att, m->qd, s);
+                                (uint16_t*)m->pf_att, xp ? (int)m->wo[l]->Kp : m->qd, xp, s);
         } else {
             float* part = (float*)device_scratch(dev, n * c.n_heads * n_splits * (hd + 2) * sizeof(float));
             int* counters = device_counters(dev, n * c.n_heads);
             launch_attn_split<true>(m->pf_q, kc, vc, true, (int)pos0, (int)n, c.n_heads, c.n_kv_heads, hd, subs,
                                     n_splits, part, counters, (void*)m->pf_att, nullptr, s);
         }
-        launch_q4_linear(m->wo[l], m->pf_att, TH_BF16, n, m->qd, m->pf_y, d, s, dev);
-        hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
-        TH_LAUNCH_CHECK();
+        if (xp_att) {  // x += att.Wo^T in the GEMM's epilogue
+            launch_q4_linear_prepared(m->wo[l], m->pf_att, n, m->pf_x, d, s, dev, true);
+        } else {
+            launch_q4_linear(m->wo[l], m->pf_att, TH_BF16, n, m->qd, m->pf_y, d, s, dev);
+            hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
+            TH_LAUNCH_CHECK();
+        }
         prefill_norm(m->ffn_norm + (size_t)l * d, m->wgu[l]);
         linear(m->wgu[l], m->pf_xb, d, m->pf_gu, 2 * ff);
         if (xp)
@@ -560,9 +565,13 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
             hipLaunchKernelGGL(prefill_swiglu_kernel<false>, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_gu, ff,
                                m->pf_sg, ff);
         TH_LAUNCH_CHECK();
-        linear(m->wd[l], m->pf_sg, ff, m->pf_y, d);
-        hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
-        TH_LAUNCH_CHECK();
+        if (xp) {  // x += sg.Wd^T in the GEMM's epilogue
+            launch_q4_linear_prepared(m->wd[l], m->pf_sg, n, m->pf_x, d, s, dev, true);
+        } else {
+            linear(m->wd[l], m->pf_sg, ff, m->pf_y, d);
+            hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
+            TH_LAUNCH_CHECK();
+        }
     }
 }
 

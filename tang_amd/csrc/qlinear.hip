@@ -113,21 +113,22 @@ static void q4_span_launch(const th_qweight* w, const void* x, size_t m, size_t 
     }
 }
 
-// Sum KS split-K partials [KS][m][ldy] in split order.
+// Sum KS split-K partials [KS][m][ldy] in split order (then add it to y when
+// add is set: the fused residual add).
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N,
-                                     int ldy, int KS) {
+                                     int ldy, int KS, int add) {
     const size_t total = (size_t)M * N;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
         const size_t m = i / N, n = i - m * N;
         float v = 0.0f;
         for (int s = 0; s < KS; s++) v += part[((size_t)s * M + m) * N + n];
-        y[m * ldy + n] = v;
+        y[m * ldy + n] = add ? y[m * ldy + n] + v : v;
     }
 }
 
 template <int RT, int CB, bool XF32, typename ST, bool XP = false>
 static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
-                           hipStream_t s, th_device* dev, bool prepared = false) {
+                           hipStream_t s, th_device* dev, bool prepared = false, bool accumulate = false) {
     if (XP && !prepared) {  // convert the activations once instead of in every column block
         const size_t total = m * (w->Kp / 8);
         uint4* xp = (uint4*)device_scratch_x(dev, total * sizeof(uint4));
@@ -155,7 +156,7 @@ static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t 
     }
     GemmDense src;
     src.M = (int)m;
-    EpiGemmStore epi{out, ldo, (size_t)m * (size_t)ldo};
+    EpiGemmStore epi{out, ldo, (size_t)m * (size_t)ldo, ks > 1 ? 0 : (int)accumulate};
     hipLaunchKernelGGL((q4_gemm_mfma_kernel<RT, CB, XF32 && !XP, ST, GemmDense, EpiGemmStore, XP>),
                        dim3(gx, gy, (unsigned)ks), dim3(256), 0, s,
                        (const uint4*)w->data, (const ST*)w->scales, x, epi, src, (int)w->rows, (int)w->cols,
@@ -165,7 +166,7 @@ static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t 
         const size_t total = m * w->rows;
         unsigned blocks = (unsigned)std::min<size_t>(ceil_div(total, 256), 4096);
         hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, out, y, (int)m, (int)w->rows,
-                           (int)ldy, (int)ks);
+                           (int)ldy, (int)ks, (int)accumulate);
         TH_LAUNCH_CHECK();
     }
 }
@@ -188,15 +189,15 @@ static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx
 }
 
 void launch_q4_linear_prepared(const th_qweight* w, const uint16_t* xp, size_t m, float* y, size_t ldy,
-                               hipStream_t s, th_device* dev) {
+                               hipStream_t s, th_device* dev, bool accumulate) {
     TH_REQUIRE(w && w->bits == 4, "not a q4 weight");
     TH_REQUIRE(m > 16, "prepared activations feed the MFMA GEMM only (m > 16)");
     if (w->scale_dtype == TH_F16) {
-        if (m <= 1024) q4_mfma_launch<2, 4, false, _Float16, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
-        else q4_mfma_launch<2, 8, false, _Float16, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
+        if (m <= 1024) q4_mfma_launch<2, 4, false, _Float16, true>(w, xp, m, w->Kp, y, ldy, s, dev, true, accumulate);
+        else q4_mfma_launch<2, 8, false, _Float16, true>(w, xp, m, w->Kp, y, ldy, s, dev, true, accumulate);
     } else {
-        if (m <= 1024) q4_mfma_launch<2, 4, false, float, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
-        else q4_mfma_launch<2, 8, false, float, true>(w, xp, m, w->Kp, y, ldy, s, dev, true);
+        if (m <= 1024) q4_mfma_launch<2, 4, false, float, true>(w, xp, m, w->Kp, y, ldy, s, dev, true, accumulate);
+        else q4_mfma_launch<2, 8, false, float, true>(w, xp, m, w->Kp, y, ldy, s, dev, true, accumulate);
     }
 }
 

@@ -844,12 +844,13 @@ struct EpiGemmStore {
     float* y;
     int ldy;
     size_t split_stride;  // split-K partials: y + blockIdx.z * split_stride
+    int add = 0;          // y += v (a residual add, device.rs:721) instead of y = v
     __device__ __forceinline__ void operator()(int out_row, int n0, int N, bool live, const float4_t& v) const {
         if (!live) return;
         float* yb = y + (size_t)blockIdx.z * split_stride + (size_t)out_row * ldy;
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            if (n0 + i < N) yb[n0 + i] = v[i];
+            if (n0 + i < N) yb[n0 + i] = add ? yb[n0 + i] + v[i] : v[i];
     }
 };
 
