@@ -39,9 +39,14 @@ struct MoeWork { int expert, slot0, rows, pad; };
 
 // Router logits: workgroup (token block, expert block); wave w takes experts
 // 4w..4w+3 of the block for ROUTER_TOK tokens; lane covers 8 consecutive
-// elements of each 512-element stride of d (f32 products, f32 sums).
+// elements of each 512-element stride of d (f32 products, f32 sums, in
+// stride order).  The loads of ROUTER_ROUND elements of d are all issued
+// before their first product, so the workgroup waits for memory once per
+// round (once at d <= ROUTER_ROUND).
+constexpr int ROUTER_ROUND = 2048;
 __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restrict__ h, const float* __restrict__ wr,
                                                          int T, int E, int d, float* __restrict__ logits) {
+    constexpr int NS = ROUTER_ROUND / 512;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t0 = blockIdx.x * ROUTER_TOK, e0 = blockIdx.y * ROUTER_EXP + wave * 4;
     float acc[ROUTER_TOK][4];
@@ -49,13 +54,29 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
     for (int a = 0; a < ROUTER_TOK; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
-    for (int k0 = lane * 8; k0 < d; k0 += 512) {
+    for (int base = 0; base < d; base += ROUTER_ROUND) {
+    uint4 hx[NS][ROUTER_TOK];
+    float4 wv[NS][4][2];
+#pragma unroll
+    for (int st = 0; st < NS; st++) {  // clamped addresses: strides past d re-read the first (not used)
+        const int k0 = (base + st * 512 + lane * 8 < d) ? base + st * 512 + lane * 8 : lane * 8;
+#pragma unroll
+        for (int a = 0; a < ROUTER_TOK; a++)
+            hx[st][a] = *(const uint4*)(h + (size_t)min(t0 + a, T - 1) * d + k0);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float* wp = wr + (size_t)min(e0 + b, E - 1) * d + k0;
+            wv[st][b][0] = *(const float4*)wp;
+            wv[st][b][1] = *(const float4*)(wp + 4);
+        }
+    }
+#pragma unroll
+    for (int st = 0; st < NS; st++) {
+        if (base + st * 512 + lane * 8 >= d) continue;
         float x[ROUTER_TOK][8];
 #pragma unroll
         for (int a = 0; a < ROUTER_TOK; a++) {
-            const int t = min(t0 + a, T - 1);
-            const uint4 v = *(const uint4*)(h + (size_t)t * d + k0);
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t w4[4] = {hx[st][a].x, hx[st][a].y, hx[st][a].z, hx[st][a].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 x[a][2 * j] = __uint_as_float(w4[j] << 16);
@@ -64,16 +85,15 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
         }
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            const int e = min(e0 + b, E - 1);
-            const float4 wa = *(const float4*)(wr + (size_t)e * d + k0);
-            const float4 wb = *(const float4*)(wr + (size_t)e * d + k0 + 4);
-            const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+            const float w8[8] = {wv[st][b][0].x, wv[st][b][0].y, wv[st][b][0].z, wv[st][b][0].w,
+                                 wv[st][b][1].x, wv[st][b][1].y, wv[st][b][1].z, wv[st][b][1].w};
 #pragma unroll
             for (int a = 0; a < ROUTER_TOK; a++)
 #pragma unroll
                 for (int j = 0; j < 8; j++) acc[a][b] = __builtin_fmaf(x[a][j], w8[j], acc[a][b]);
         }
     }
+    }  // rounds
 #pragma unroll
     for (int a = 0; a < ROUTER_TOK; a++)
 #pragma unroll
@@ -84,13 +104,12 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
 }
 
 // Softmax over the E logits (max, exp, sum, scale by 1/sum, as cpu.rs:105-124)
-// and top-k by probability, first maximum on ties (sampling.rs:184-194).  One
-// wave per token; lane holds experts lane, lane+64, ...
-__global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
-                                                       int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+// and top-k by probability, first maximum on ties (sampling.rs:184-194), for
+// token t by one wave; lane holds experts lane, lane+64, ...  Lane 0 writes
+// entry r of the token to idx[r], w[r].
+__device__ __forceinline__ void moe_topk_token(const float* __restrict__ logits, int t, int E, int k, int32_t* idx,
+                                               float* w) {
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;
     constexpr int PL = MOE_MAX_E / 64;
     float p[PL];
     float mx = -INFINITY;
@@ -126,13 +145,20 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
         if (lane == 0) {
-            topk_idx[(size_t)t * k + r] = bi;
-            topk_w[(size_t)t * k + r] = bv;
+            idx[r] = bi;
+            w[r] = bv;
         }
 #pragma unroll
         for (int i = 0; i < PL; i++)
             if (lane + 64 * i == bi) p[i] = -INFINITY;  // taken; -inf never beats a live expert's p >= 0
     }
+}
+
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                       int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    moe_topk_token(logits, t, E, k, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
 }
 
 // Slot assignment, deterministic: slots are grouped by expert (routed
@@ -142,13 +168,32 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
 // with eight ballots over the expert id bits, so ranks inside a batch come
 // from popcounts, and per-(wave, expert) counts give each wave its first slot.
 // Work items cover at most `rows` slots of one expert.
-__global__ __launch_bounds__(1024) void moe_dispatch_kernel(const int32_t* __restrict__ topk_idx, int T, int k, int E,
+// With logits set (T * k <= MOE_FUSED_ENTRIES), the block first runs the
+// top-k itself (wave w takes tokens w, w+16, ...), writes topk_idx/topk_w
+// and keeps the indices in LDS for the slot passes: one launch instead of two
+// for decode-sized batches.
+constexpr int MOE_FUSED_ENTRIES = 1024;
+__global__ __launch_bounds__(1024) void moe_dispatch_kernel(const float* __restrict__ logits, int32_t* __restrict__ topk_idx_out,
+                                                            float* __restrict__ topk_w_out,
+                                                            const int32_t* __restrict__ topk_idx_in, int T, int k, int E,
                                                             int S, int rows, int* __restrict__ offsets,
                                                             int* __restrict__ slot_token, int* __restrict__ token_slot,
                                                             MoeWork* __restrict__ work, int max_work) {
     __shared__ int cnt[16][MOE_MAX_E];  // per-wave counts, then per-wave running slots
     __shared__ int tot[MOE_MAX_NE], base[MOE_MAX_NE + 1], wbase[MOE_MAX_NE + 1];
+    __shared__ int32_t sidx[MOE_FUSED_ENTRIES];
+    __shared__ float sw[MOE_FUSED_ENTRIES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NE = E + S;
+    const int32_t* topk_idx = topk_idx_in;
+    if (logits) {
+        for (int t = wave; t < T; t += 16) moe_topk_token(logits, t, E, k, sidx + t * k, sw + t * k);
+        __syncthreads();
+        for (int i = tid; i < T * k; i += 1024) {
+            topk_idx_out[i] = sidx[i];
+            topk_w_out[i] = sw[i];
+        }
+        topk_idx = sidx;
+    }
     const int n = T * k, per = (n + 15) / 16;
     const int lo = wave * per, hi = min(n, lo + per);
     for (int i = tid; i < 16 * MOE_MAX_E; i += 1024) (&cnt[0][0])[i] = 0;
@@ -557,10 +602,14 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
     hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)ceil_div(T, ROUTER_TOK), (unsigned)ceil_div(m->E, ROUTER_EXP)),
                        dim3(256), 0, s, (const uint16_t*)h->ptr, m->router, (int)T, (int)m->E, (int)m->d, m->logits);
     TH_LAUNCH_CHECK();
-    hipLaunchKernelGGL(moe_topk_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, s, m->logits, (int)T, (int)m->E,
-                       (int)m->k, (int32_t*)topk_idx->ptr, (float*)topk_w->ptr);
-    TH_LAUNCH_CHECK();
-    hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(1024), 0, s, (const int32_t*)topk_idx->ptr, (int)T, (int)m->k,
+    const bool fused = T * m->k <= (size_t)MOE_FUSED_ENTRIES && T <= (size_t)MOE_SMALL_T;  // top-k inside dispatch
+    if (!fused) {
+        hipLaunchKernelGGL(moe_topk_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, s, m->logits, (int)T,
+                           (int)m->E, (int)m->k, (int32_t*)topk_idx->ptr, (float*)topk_w->ptr);
+        TH_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(1024), 0, s, fused ? (const float*)m->logits : nullptr,
+                       (int32_t*)topk_idx->ptr, (float*)topk_w->ptr, (const int32_t*)topk_idx->ptr, (int)T, (int)m->k,
                        (int)m->E, (int)m->S, rows, m->offsets, m->slot_token, m->token_slot, m->work, (int)max_work);
     TH_LAUNCH_CHECK();
     const uint16_t* hx = (const uint16_t*)h->ptr;
