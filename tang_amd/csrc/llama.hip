@@ -277,27 +277,24 @@ __global__ void prefill_add_kernel(float* __restrict__ x, const float* __restric
 // SwiGLU of the interleaved gate/up rows (tile b: gate 8b..8b+7, up
 // 8b..8b+7) to the down-projection input, rounded to bf16: as bf16 rows of
 // ldo, or (XP) in the MFMA GEMM's prepared f16 layout (zero past ff).  One
-// thread per 8-value chunk; ff % 8 == 0.
+// thread per value (f64 math, as cpu.rs:68); in XP mode lane i < 4 of each
+// aligned group of 8 pairs its value with lane i+4's and stores that dword.
+// ldo % 8 == 0, ff % 8 == 0; the launch's x extent is a multiple of 8 threads.
 template <bool XP>
 __global__ void prefill_swiglu_kernel(const float* __restrict__ gu, int ff, uint16_t* __restrict__ out, int ldo) {
     const int row = blockIdx.y;
     const float* g = gu + (size_t)row * 2 * ff;
     uint16_t* orow = out + (size_t)row * ldo;
-    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c * 8 < ldo; c += gridDim.x * blockDim.x) {
-        const int b = c;  // chunk c = tile c's eight gate/up pairs
-        float y[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            y[i] = c * 8 < ff ? bf16_bits_to_f32(f32_to_bf16_rne(swiglu_f64(g[16 * b + i], g[16 * b + 8 + i]))) : 0.0f;
+    const int lim = XP ? ldo : ff;
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < lim; j += gridDim.x * blockDim.x) {
+        const int b = j >> 3, rr = j & 7;
+        const uint16_t hb = j < ff ? f32_to_bf16_rne(swiglu_f64(g[16 * b + rr], g[16 * b + 8 + rr])) : 0;
         if (XP) {
-            *(uint4*)(orow + c * 8) = make_uint4(pack_half2(y[0], y[4]), pack_half2(y[1], y[5]),
-                                                 pack_half2(y[2], y[6]), pack_half2(y[3], y[7]));
-        } else if (c * 8 < ff) {
-            uint32_t o[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                o[i] = (uint32_t)f32_to_bf16_rne(y[2 * i]) | ((uint32_t)f32_to_bf16_rne(y[2 * i + 1]) << 16);
-            *(uint4*)(orow + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+            const float y = __uint_as_float((uint32_t)hb << 16);
+            const float z = __shfl_down(y, 4, 8);  // the value 4 further along the chunk
+            if (rr < 4) *(uint32_t*)(orow + 8 * b + 2 * rr) = pack_half2(y, z);
+        } else {
+            orow[j] = hb;
         }
     }
 }
