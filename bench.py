@@ -33,7 +33,7 @@ GEMV_BYTES = {1: 25414656, 4: 25571328, 8: 25780224, 16: 26198016}  # algorithmi
 N_COPIES = 12  # 12 x 25.4 MB = 305 MB > 256 MB last-level cache
 # HBM bytes per M=1 launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE runs in
 # profiles/q4_gemv_config2.md, each scaled by its reading of a known-size copy.
-TRAFFIC_BYTES = 25568256
+TRAFFIC_BYTES = 25563136
 
 CFG7B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=32, head_dim=128, d_ff=11008, vocab=32000,
              max_seq=2176, eps=1e-5, rope_theta=1e4)
@@ -257,6 +257,8 @@ def main():
     ap.add_argument("--no-moe-mla", action="store_true")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="counter runs: 240 GEMV launches, then one 256 MiB device copy as the traffic calibration")
+    ap.add_argument("--profile-gemm", action="store_true",
+                    help="counter runs: four M=2048 prefill GEMMs on the config-2 matrix")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (collectives are out of scope); "
@@ -264,6 +266,9 @@ def main():
         sys.exit(2)
 
     dev = capi.HipComputeDevice(0)
+    if args.profile_gemm:
+        print(json.dumps(prefill_bench(dev, 2048, steps=4)))
+        return
     if args.profile_gemv:
         gemv_bench(dev, 1, 240, 0, graph=False)  # kernel tracers do not follow graph replays
         a, b = dev.alloc(256 << 20, capi.U8), dev.alloc(256 << 20, capi.U8)
