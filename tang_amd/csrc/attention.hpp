@@ -388,17 +388,18 @@ inline void launch_attn_prefill(const float* q, int ldq, const _Float16* kc, con
 // for every position); splits past it only write an empty record.  (Sharing
 // the length evenly over all n_splits workgroups was measured slower: more
 // workgroups each paying the record and merge overhead.)
-template <int D, int SPL, bool OUT_BF16>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
+template <int D, int SPL, bool OUT_BF16, int NT>
+__global__ __launch_bounds__(NT) void attn_decode_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                           const _Float16* __restrict__ vc, int n_heads, int n_kv_heads,
                                                           int n_splits, float* __restrict__ part,
                                                           int* __restrict__ counters, void* __restrict__ out,
                                                           const int* __restrict__ cache_start_dev) {
     constexpr int LPK = D / 8;           // lanes per key (eight elements each)
-    constexpr int KPB = 256 / LPK;       // keys per block pass
+    constexpr int NWV = NT / 64;         // waves
+    constexpr int KPB = NT / LPK;        // keys per block pass
     constexpr int KPT = SPL / KPB;       // keys per thread
     static_assert(KPT >= 1 && KPT * KPB == SPL && LPK <= 64 && 64 % LPK == 0, "bad split shape");
-    __shared__ float red[2][4];
+    __shared__ float red[2][NWV];
     __shared__ float vacc[KPB][D + 1];
     __shared__ int s_last;
     const int h = blockIdx.x, s = blockIdx.z;
@@ -412,7 +413,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     float* recs = part + (size_t)h * n_splits * (D + 2);
     float* rec = recs + (size_t)s * (D + 2);
     if (len == 0) {
-        for (int i = tid; i < D + 2; i += 256) st_coherent(&rec[i], i == 0 ? -INFINITY : 0.0f);
+        for (int i = tid; i < D + 2; i += NT) st_coherent(&rec[i], i == 0 ? -INFINITY : 0.0f);
     } else {
         // Issue order = use order (loads complete in order): q, every K row,
         // then every V row, so the scores start while V is still streaming.
@@ -459,7 +460,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
         for (int o = LPK; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
         if (lane == 0) red[0][wave] = mx;
         __syncthreads();
-        const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+        float M = red[0][0];
+#pragma unroll
+        for (int w = 1; w < NWV; w++) M = fmaxf(M, red[0][w]);
         float acc[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[i] = 0.0f;
@@ -481,7 +484,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
 #pragma unroll
         for (int i = 0; i < 8; i++) vacc[slot][e * 8 + i] = acc[i];
         __syncthreads();
-        for (int d = tid; d < D; d += 256) {
+        for (int d = tid; d < D; d += NT) {
             float v = 0.0f;
 #pragma unroll
             for (int k = 0; k < KPB; k++) v += vacc[k][d];
@@ -489,29 +492,29 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
         }
         if (tid == 0) {
             st_coherent(&rec[0], M);
-            st_coherent(&rec[1], (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]));
+            st_coherent(&rec[1], tree_sum<NWV>(red[1]));  // fixed pairwise order
         }
     }
     if (!last_arrival(&counters[h], n_splits, &s_last)) return;
     extern __shared__ float recl[];  // [n_splits][D + 2]
-    __shared__ float redm[256];
+    __shared__ float redm[NWV];
     const int total = n_splits * (D + 2);
-    ld_coherent_to_lds(recs, total, recl, tid);
+    ld_coherent_to_lds<NT>(recs, total, recl, tid);
     __syncthreads();
     float mloc = -INFINITY;
-    for (int i = tid; i < n_splits; i += 256) mloc = fmaxf(mloc, recl[(size_t)i * (D + 2)]);
-    const float Mx = block_max_256(mloc, redm);
+    for (int i = tid; i < n_splits; i += NT) mloc = fmaxf(mloc, recl[(size_t)i * (D + 2)]);
+    const float Mx = block_max_n<NT>(mloc, redm);
     float lloc = 0.0f;
     __shared__ float wts[256];
-    for (int i = tid; i < n_splits; i += 256) {
+    for (int i = tid; i < n_splits; i += NT) {
         const float m = recl[(size_t)i * (D + 2)];
         const float w = m == -INFINITY ? 0.0f : expf(m - Mx);
         wts[i] = w;
         lloc += w * recl[(size_t)i * (D + 2) + 1];
     }
-    const float L = block_sum_256(lloc, redm);  // its barriers also publish wts
+    const float L = block_sum_n<NT>(lloc, redm);  // its barriers also publish wts
     const float inv = 1.0f / L;
-    for (int d = tid; d < D; d += 256) {
+    for (int d = tid; d < D; d += NT) {
         float a = 0.0f;
         for (int i = 0; i < n_splits; i++) a += recl[(size_t)i * (D + 2) + 2 + d] * wts[i];
         const size_t o = (size_t)h * D + d;
@@ -565,7 +568,7 @@ inline void launch_attn_split(const float* q, const void* kc, const void* vc, bo
 
 // Decode attention for the engine: one query, f16 cache, SPL positions per
 // split; counters (n_heads ints) zero on entry and on return.
-template <int SPL, bool OUT_BF16>
+template <int SPL, bool OUT_BF16, int NT = 256>
 inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float16* vc, int n_heads, int n_kv_heads,
                                int head_dim, int n_splits, float* part, int* counters, void* out,
                                const int* cache_start_dev, hipStream_t s) {
@@ -574,9 +577,9 @@ inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float1
     const size_t lds = attn_merge_lds(n_splits, head_dim);
     TH_REQUIRE(lds <= 48 * 1024, "too many attention splits for the LDS merge");
     switch (head_dim) {
-        case 64: hipLaunchKernelGGL((attn_decode_kernel<64, SPL, OUT_BF16>), grid, dim3(256), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 128: hipLaunchKernelGGL((attn_decode_kernel<128, SPL, OUT_BF16>), grid, dim3(256), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 256: hipLaunchKernelGGL((attn_decode_kernel<256, SPL, OUT_BF16>), grid, dim3(256), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 64: hipLaunchKernelGGL((attn_decode_kernel<64, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 128: hipLaunchKernelGGL((attn_decode_kernel<128, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 256: hipLaunchKernelGGL((attn_decode_kernel<256, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
         default: throw Error(TH_ERR_INVALID, "launch_attn_decode: unsupported head_dim");
     }
     TH_LAUNCH_CHECK();

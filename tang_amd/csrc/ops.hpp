@@ -53,16 +53,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // Same coherence as ld_coherent, but plain buffer loads, which the compiler
 // does not serialise (atomic loads each wait for the previous one): sixteen
 // per thread are in flight per round.  Call with the whole 256-thread block.
+template <int NT = 256>
 __device__ __forceinline__ void ld_coherent_to_lds(const float* src, int n, float* dst, int tid) {
     const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(src, (uint32_t)n * 4u);
-    for (int base = 0; base < n; base += 16 * 256) {
+    for (int base = 0; base < n; base += 16 * NT) {
         float v[16];
 #pragma unroll
         for (int u = 0; u < 16; u++)  // past n: out of the resource, reads 0
-            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (base + tid + u * 256) * 4, 0, CPOL_SC1));
+            v[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (base + tid + u * NT) * 4, 0, CPOL_SC1));
 #pragma unroll
         for (int u = 0; u < 16; u++)
-            if (base + tid + u * 256 < n) dst[base + tid + u * 256] = v[u];
+            if (base + tid + u * NT < n) dst[base + tid + u * NT] = v[u];
     }
 }
 // Count this workgroup's arrival; true in the last of `total` to arrive
@@ -90,6 +91,36 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
+}
+
+// Pairwise sum of n (a power of two) values: ((r0+r1)+(r2+r3))+...
+template <int N>
+__device__ __forceinline__ float tree_sum(const float* r) {
+    if constexpr (N == 1) return r[0];
+    else return tree_sum<N / 2>(r) + tree_sum<N / 2>(r + N / 2);
+}
+
+// Sum / max over an NT-thread block in a fixed order; every thread gets it.
+template <int NT>
+__device__ __forceinline__ float block_sum_n(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return tree_sum<NT / 64>(red);
+}
+template <int NT>
+__device__ __forceinline__ float block_max_n(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) m = fmaxf(m, red[w]);
+    return m;
 }
 
 // Sum over a 256-thread block; every thread gets the result.
