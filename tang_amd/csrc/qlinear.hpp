@@ -657,7 +657,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
                                                       const float* __restrict__ sc,
                                                       const void* __restrict__ xin, int K, int Kp,
                                                       int N, int ldx, Epi epi) {
-    constexpr int D = 8;
+    constexpr int D = 4;  // weight chunks in flight per wave (2: 7.5 us, 4: 5.8, 6: 6.0, 8: 5.9, 16: 7.3 on config 1)
     constexpr int XB = 4;  // 16-element x chunks per thread loaded ahead of the weights
     extern __shared__ uint4 smem[];
     const int NCH = Kp >> 6;  // 64-element chunks
