@@ -203,16 +203,20 @@ def _prefill(m, cfg, toks, pos):
     return nxt.value, logits
 
 
-@pytest.mark.parametrize("n", [1, 37, 600])  # 600: two prompt chunks of the M=n GEMM path
-def test_small_llama_prefill_matches_oracle(dev, n):
-    """th_llama_prefill (M=n GEMMs, causal split attention, K/V appended)
-    against the oracle fed the same tokens one decode step at a time: the
-    last logits within the bf16-activation bar, the same next token, and 12
-    greedy decode steps continuing from the state prefill leaves (which
-    read the K/V rows prefill wrote) match the oracle's continuation."""
+@pytest.mark.parametrize("n,hd", [(1, 64), (37, 64), (600, 64), (37, 256)])
+def test_small_llama_prefill_matches_oracle(dev, n, hd):
+    """th_llama_prefill (M=n GEMMs, causal attention, K/V appended) against
+    the oracle fed the same tokens one decode step at a time: the last logits
+    within the bf16-activation bar, the same next token, and 12 greedy decode
+    steps continuing from the state prefill leaves (which read the K/V rows
+    prefill wrote) match the oracle's continuation.  n=600 runs two prompt
+    chunks; head_dim 64 takes the MFMA flash attention, 256 the split
+    attention (one head of 256)."""
     cfg = dict(CONFIG_SMALL, max_seq=max(CONFIG_SMALL["max_seq"], 100 + n + 16))
+    if hd != CONFIG_SMALL["head_dim"]:
+        cfg.update(n_heads=CONFIG_SMALL["d_model"] // hd, n_kv_heads=1, head_dim=hd)
     prefill, steps = 100, 12
-    print(f"prefill n={n}", flush=True)
+    print(f"prefill n={n} head_dim={hd}", flush=True)
     rng = np.random.default_rng(n)
     toks = [int(t) for t in rng.integers(0, cfg["vocab"], n)]
     ref = OracleLlama(cfg, 7, 8, prefill)
