@@ -38,7 +38,7 @@ static void q4_gemv_launch_v(const th_qweight* w, const void* x, size_t ldx, flo
         set_smem(k, smem);
         hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(1024), smem, s, (const uint4*)w->data,
                            (const ST*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi, NormArgs{}, src);
-    } else if (M >= 8 || w->Np / 16 < 512) {  // few tiles, or big LDS staging: split K over eight waves per tile
+    } else if (MR >= 3 || w->Np / 16 < 512) {  // few tiles, or 3+ staged rows: split K over eight waves per tile
         const size_t smem = Q4GemvSmem<MR, 8>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
         auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, 4, 8, false, Src>;
