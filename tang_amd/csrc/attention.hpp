@@ -444,14 +444,13 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(const float* __restrict
 #pragma unroll
         for (int k = 0; k < KPT; k++) {
             const uint32_t w[4] = {kr[k].x, kr[k].y, kr[k].z, kr[k].w};
-            float d = 0.0f;
+            float d = 0.0f;  // mixed-precision FMAs: the f16 operand is read in place
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                d += qv[2 * i] * (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFF));
-                d += qv[2 * i + 1] * (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+                d = __builtin_fmaf(qv[2 * i], (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFF)), d);
+                d = __builtin_fmaf(qv[2 * i + 1], (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16)), d);
             }
-#pragma unroll
-            for (int o = LPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+            d = group_sum<LPK>(d);
             sc[k] = slot + k * KPB < len ? d * scale : -INFINITY;
             mx = fmaxf(mx, sc[k]);
         }
@@ -496,30 +495,43 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(const float* __restrict
         }
     }
     if (!last_arrival(&counters[h], n_splits, &s_last)) return;
-    extern __shared__ float recl[];  // [n_splits][D + 2]
-    __shared__ float redm[NWV];
-    const int total = n_splits * (D + 2);
-    ld_coherent_to_lds<NT>(recs, total, recl, tid);
-    __syncthreads();
-    float mloc = -INFINITY;
-    for (int i = tid; i < n_splits; i += NT) mloc = fmaxf(mloc, recl[(size_t)i * (D + 2)]);
-    const float Mx = block_max_n<NT>(mloc, redm);
-    float lloc = 0.0f;
-    __shared__ float wts[256];
-    for (int i = tid; i < n_splits; i += NT) {
-        const float m = recl[(size_t)i * (D + 2)];
-        const float w = m == -INFINITY ? 0.0f : expf(m - Mx);
-        wts[i] = w;
-        lloc += w * recl[(size_t)i * (D + 2) + 1];
-    }
-    const float L = block_sum_n<NT>(lloc, redm);  // its barriers also publish wts
-    const float inv = 1.0f / L;
+    // Merge in the last split to arrive: thread d combines column d of the
+    // splits that hold keys (the others wrote empty records), sixteen splits
+    // per round of coherent loads, with a running max; every thread forms
+    // the same M and L in the same order.
+    const int ns = min(n_splits, (attend + SPL - 1) / SPL);
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(recs, (uint32_t)(ns * (D + 2)) * 4u);
     for (int d = tid; d < D; d += NT) {
-        float a = 0.0f;
-        for (int i = 0; i < n_splits; i++) a += recl[(size_t)i * (D + 2) + 2 + d] * wts[i];
-        const size_t o = (size_t)h * D + d;
-        if (OUT_BF16) ((uint16_t*)out)[o] = f32_to_bf16_rne(a * inv);
-        else ((float*)out)[o] = a * inv;
+        float M = -INFINITY, L = 0.0f, A = 0.0f;
+        for (int c = 0; c < ns; c += 16) {
+            float m[16], l[16], o[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {  // past ns: outside the resource, reads 0 (masked below)
+                const int off = ((c + u) * (D + 2)) * 4;
+                m[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, CPOL_SC1));
+                l[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off + 4, 0, CPOL_SC1));
+                o[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off + 8 + 4 * d, 0, CPOL_SC1));
+            }
+            float cm = M;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (c + u < ns) cm = fmaxf(cm, m[u]);
+            const float r = expf(M - cm);  // 0 on the first round (M = -inf)
+            L *= r;
+            A *= r;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (c + u < ns) {
+                    const float w = expf(m[u] - cm);
+                    L = __builtin_fmaf(w, l[u], L);
+                    A = __builtin_fmaf(w, o[u], A);
+                }
+            M = cm;
+        }
+        const float v = A * (1.0f / L);
+        const size_t oi = (size_t)h * D + d;
+        if (OUT_BF16) ((uint16_t*)out)[oi] = f32_to_bf16_rne(v);
+        else ((float*)out)[oi] = v;
     }
 }
 
@@ -574,8 +586,7 @@ inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float1
                                const int* cache_start_dev, hipStream_t s) {
     TH_REQUIRE(n_splits >= 1 && n_splits <= 256, "attention split count out of range");
     const dim3 grid((unsigned)n_heads, 1, (unsigned)n_splits);
-    const size_t lds = attn_merge_lds(n_splits, head_dim);
-    TH_REQUIRE(lds <= 48 * 1024, "too many attention splits for the LDS merge");
+    const size_t lds = 0;
     switch (head_dim) {
         case 64: hipLaunchKernelGGL((attn_decode_kernel<64, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
         case 128: hipLaunchKernelGGL((attn_decode_kernel<128, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;

@@ -604,8 +604,7 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
     TH_REQUIRE(c.n_heads * c.head_dim == c.d_model, "n_heads*head_dim must equal d_model");
     TH_REQUIRE(c.d_ff % 8 == 0 && c.d_model % 16 == 0, "d_model must be a multiple of 16 and d_ff of 8");
     TH_REQUIRE(c.d_model <= 4096, "the RMSNorm prologue supports d_model <= 4096");
-    TH_REQUIRE(attn_merge_lds((int)ceil_div((size_t)c.max_seq, ATTN_SPLIT_ENGINE), c.head_dim) <= 48 * 1024,
-               "max_seq too long for the attention merge");
+    TH_REQUIRE(ceil_div((size_t)c.max_seq, (size_t)ATTN_SPLIT_ENGINE) <= 256, "max_seq too long for the attention splits");
     th_llama* m = new th_llama();
     try {
         m->dev = dev;

@@ -81,6 +81,25 @@ __device__ __forceinline__ bool last_arrival(int* counter, int total, int* s_fla
     return *s_flag != 0;
 }
 
+// One DPP move inside rows of 16 lanes (CTRL: the dpp_ctrl encoding).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of N lanes (N a power of two up to 64) on the VALU:
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror,
+// then cross-row shuffles.  Every lane of a group gets the same value.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (N >= 2) v += dpp_move<0xB1>(v);
+    if constexpr (N >= 4) v += dpp_move<0x4E>(v);
+    if constexpr (N >= 8) v += dpp_move<0x141>(v);
+    if constexpr (N >= 16) v += dpp_move<0x140>(v);
+    if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 // Wave-level sum: row-local DPP-free butterfly over 64 lanes.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
