@@ -33,12 +33,13 @@ constexpr int MOE_SMALL_T = 64;     // batches up to this use MOE_MIN_ROWS, larg
 constexpr int MOE_MAX_E = 256;      // routed experts (top-k runs in one wave, 4 per lane)
 constexpr int MOE_MAX_NE = 1024;    // routed + shared
 constexpr int ROUTER_TOK = 4;       // tokens per router workgroup
-constexpr int ROUTER_EXP = 16;      // experts per router workgroup (4 per wave)
+constexpr int ROUTER_EXP = 4;       // experts per router workgroup (one per wave)
 
 struct MoeWork { int expert, slot0, rows, pad; };
 
-// Router logits: workgroup (token block, expert block); wave w takes experts
-// 4w..4w+3 of the block for ROUTER_TOK tokens; lane covers 8 consecutive
+// Router logits: workgroup (token block, expert block); wave w takes expert
+// w of the block for ROUTER_TOK tokens (decode-sized batches then spread over
+// E * T / 16 workgroups instead of a handful); lane covers 8 consecutive
 // elements of each 512-element stride of d (f32 products, f32 sums, in
 // stride order).  The loads of ROUTER_ROUND elements of d are all issued
 // before their first product, so the workgroup waits for memory once per
@@ -47,16 +48,17 @@ constexpr int ROUTER_ROUND = 2048;
 __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restrict__ h, const float* __restrict__ wr,
                                                          int T, int E, int d, float* __restrict__ logits) {
     constexpr int NS = ROUTER_ROUND / 512;
+    constexpr int EPW = ROUTER_EXP / 4;  // experts per wave
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t0 = blockIdx.x * ROUTER_TOK, e0 = blockIdx.y * ROUTER_EXP + wave * 4;
-    float acc[ROUTER_TOK][4];
+    const int t0 = blockIdx.x * ROUTER_TOK, e0 = blockIdx.y * ROUTER_EXP + wave * EPW;
+    float acc[ROUTER_TOK][EPW];
 #pragma unroll
     for (int a = 0; a < ROUTER_TOK; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+        for (int b = 0; b < EPW; b++) acc[a][b] = 0.0f;
     for (int base = 0; base < d; base += ROUTER_ROUND) {
     uint4 hx[NS][ROUTER_TOK];
-    float4 wv[NS][4][2];
+    float4 wv[NS][EPW][2];
 #pragma unroll
     for (int st = 0; st < NS; st++) {  // clamped addresses: strides past d re-read the first (not used)
         const int k0 = (base + st * 512 + lane * 8 < d) ? base + st * 512 + lane * 8 : lane * 8;
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
         for (int a = 0; a < ROUTER_TOK; a++)
             hx[st][a] = *(const uint4*)(h + (size_t)min(t0 + a, T - 1) * d + k0);
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
+        for (int b = 0; b < EPW; b++) {
             const float* wp = wr + (size_t)min(e0 + b, E - 1) * d + k0;
             wv[st][b][0] = *(const float4*)wp;
             wv[st][b][1] = *(const float4*)(wp + 4);
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
             }
         }
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
+        for (int b = 0; b < EPW; b++) {
             const float w8[8] = {wv[st][b][0].x, wv[st][b][0].y, wv[st][b][0].z, wv[st][b][0].w,
                                  wv[st][b][1].x, wv[st][b][1].y, wv[st][b][1].z, wv[st][b][1].w};
 #pragma unroll
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
 #pragma unroll
     for (int a = 0; a < ROUTER_TOK; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
+        for (int b = 0; b < EPW; b++) {
             const float v = wave_sum(acc[a][b]);
             if (lane == 0 && t0 + a < T && e0 + b < E) logits[(size_t)(t0 + a) * E + e0 + b] = v;
         }
@@ -105,10 +107,15 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
 
 // Softmax over the E logits (max, exp, sum, scale by 1/sum, as cpu.rs:105-124)
 // and top-k by probability, first maximum on ties (sampling.rs:184-194), for
-// token t by one wave; lane holds experts lane, lane+64, ...  Lane 0 writes
-// entry r of the token to idx[r], w[r].
+// token t by one wave; lane holds experts lane, lane+64, ...  Repeated
+// argmax picks experts in order of (probability descending, index
+// ascending), so each expert's pick index is its rank in that order: the
+// number of experts with a larger probability, or an equal one and a lower
+// index.  Every lane counts its experts' ranks against the probabilities in
+// the wave's LDS row sp[E] (no serial reductions); the expert of rank r < k
+// writes entry r of the token to idx[r], w[r].
 __device__ __forceinline__ void moe_topk_token(const float* __restrict__ logits, int t, int E, int k, int32_t* idx,
-                                               float* w) {
+                                               float* w, float* sp) {
     const int lane = threadIdx.x & 63;
     constexpr int PL = MOE_MAX_E / 64;
     float p[PL];
@@ -119,46 +126,59 @@ __device__ __forceinline__ void moe_topk_token(const float* __restrict__ logits,
         p[i] = e < E ? logits[(size_t)t * E + e] : -INFINITY;
         mx = fmaxf(mx, p[i]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = group_max<64>(mx);
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < PL; i++) {
         p[i] = lane + 64 * i < E ? expf(p[i] - mx) : 0.0f;
         sum += p[i];
     }
-    sum = wave_sum(sum);
+    sum = group_sum<64>(sum);
     const float inv = 1.0f / sum;
+    const int E16 = (E + 15) & ~15;  // sp is padded to whole 16-float rounds with -inf
 #pragma unroll
-    for (int i = 0; i < PL; i++) p[i] = lane + 64 * i < E ? p[i] * inv : -INFINITY;
-    for (int r = 0; r < k; r++) {
-        // lane's best (lowest index on ties), then the wave's
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < PL; i++)
-            if (p[i] > bv || (p[i] == bv && bi == 0x7fffffff && lane + 64 * i < E)) { bv = p[i]; bi = lane + 64 * i; }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if (lane == 0) {
-            idx[r] = bi;
-            w[r] = bv;
-        }
-#pragma unroll
-        for (int i = 0; i < PL; i++)
-            if (lane + 64 * i == bi) p[i] = -INFINITY;  // taken; -inf never beats a live expert's p >= 0
+    for (int i = 0; i < PL; i++) {
+        p[i] = p[i] * inv;
+        const int e = lane + 64 * i;
+        if (e < E16) sp[e] = e < E ? p[i] : -INFINITY;
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    const int pl = (E + 63) >> 6;  // lane slots holding experts
+    int rank[PL];
+#pragma unroll
+    for (int i = 0; i < PL; i++) rank[i] = 0;
+    for (int j0 = 0; j0 < E16; j0 += 16) {
+        float pj[16];  // same addresses in every lane: broadcast reads, all issued first
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float4 v = *(const float4*)(sp + j0 + 4 * u);
+            pj[4 * u] = v.x; pj[4 * u + 1] = v.y; pj[4 * u + 2] = v.z; pj[4 * u + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < PL; i++)
+            if (i < pl) {
+                const int e = lane + 64 * i;
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    rank[i] += (pj[u] > p[i] || (pj[u] == p[i] && j0 + u < e)) ? 1 : 0;
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < PL; i++)
+        if (lane + 64 * i < E && rank[i] < k) {
+            idx[rank[i]] = lane + 64 * i;
+            w[rank[i]] = p[i];
+        }
 }
 
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                        int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+    __shared__ __align__(16) float sp[4][MOE_MAX_E];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    moe_topk_token(logits, t, E, k, topk_idx + (size_t)t * k, topk_w + (size_t)t * k);
+    moe_topk_token(logits, t, E, k, topk_idx + (size_t)t * k, topk_w + (size_t)t * k, sp[threadIdx.x >> 6]);
 }
 
 // Slot assignment, deterministic: slots are grouped by expert (routed
@@ -179,14 +199,16 @@ __global__ __launch_bounds__(1024) void moe_dispatch_kernel(const float* __restr
                                                             int S, int rows, int* __restrict__ offsets,
                                                             int* __restrict__ slot_token, int* __restrict__ token_slot,
                                                             MoeWork* __restrict__ work, int max_work) {
-    __shared__ int cnt[16][MOE_MAX_E];  // per-wave counts, then per-wave running slots
+    __shared__ __align__(16) int cnt[16][MOE_MAX_E];  // per-wave counts, then per-wave running slots
     __shared__ int tot[MOE_MAX_NE], base[MOE_MAX_NE + 1], wbase[MOE_MAX_NE + 1];
     __shared__ int32_t sidx[MOE_FUSED_ENTRIES];
     __shared__ float sw[MOE_FUSED_ENTRIES];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NE = E + S;
     const int32_t* topk_idx = topk_idx_in;
     if (logits) {
-        for (int t = wave; t < T; t += 16) moe_topk_token(logits, t, E, k, sidx + t * k, sw + t * k);
+        // the wave's row of cnt (zeroed below) holds its probabilities
+        for (int t = wave; t < T; t += 16)
+            moe_topk_token(logits, t, E, k, sidx + t * k, sw + t * k, (float*)cnt[wave]);
         __syncthreads();
         for (int i = tid; i < T * k; i += 1024) {
             topk_idx_out[i] = sidx[i];
@@ -225,13 +247,22 @@ __global__ __launch_bounds__(1024) void moe_dispatch_kernel(const float* __restr
         tot[e] = c;
     }
     __syncthreads();
-    if (tid == 0) {  // exclusive scans of slots and of work items over experts
-        int o = 0, wo = 0;
-        for (int e = 0; e < NE; e++) {
-            base[e] = o; wbase[e] = wo;
-            o += tot[e]; wo += (tot[e] + rows - 1) / rows;
+    {  // exclusive scans of slots and of work items over experts (NE <= 1024: one per thread)
+        __shared__ int wsum[2][16];
+        const int tv = tid < NE ? tot[tid] : 0;
+        const int wv = (tv + rows - 1) / rows;
+        int a = tv, b = wv;  // inclusive scans within the wave
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int ta = __shfl_up(a, o, 64), tb = __shfl_up(b, o, 64);
+            if (lane >= o) { a += ta; b += tb; }
         }
-        base[NE] = o; wbase[NE] = wo;
+        if (lane == 63) { wsum[0][wave] = a; wsum[1][wave] = b; }
+        __syncthreads();
+        int oa = 0, ob = 0;
+        for (int w = 0; w < wave; w++) { oa += wsum[0][w]; ob += wsum[1][w]; }
+        if (tid < NE) { base[tid] = oa + a - tv; wbase[tid] = ob + b - wv; }
+        if (tid == NE - 1) { base[NE] = oa + a; wbase[NE] = ob + b; }
     }
     __syncthreads();
     for (int e = tid; e <= NE; e += 1024) offsets[e] = base[e];

@@ -100,6 +100,17 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (N >= 2) v = fmaxf(v, dpp_move<0xB1>(v));
+    if constexpr (N >= 4) v = fmaxf(v, dpp_move<0x4E>(v));
+    if constexpr (N >= 8) v = fmaxf(v, dpp_move<0x141>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp_move<0x140>(v));
+    if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
 // Wave-level sum: row-local DPP-free butterfly over 64 lanes.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
