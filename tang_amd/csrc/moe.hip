@@ -535,6 +535,7 @@ static void moe_grouped_gemm(const th_moe* m, const th_qweight* w0, const uint4*
                              size_t max_work, Epi epi) {
     // the x_rows activation rows (tokens, or slots) converted to f16 once
     const size_t total = x_rows * (w0->Kp / 8);
+    TH_REQUIRE(total * sizeof(uint4) < 0x7FFFFFF0u, "prepared activations above 2 GiB");  // 32-bit buffer offsets
     uint4* xp = (uint4*)device_scratch_x(m->dev, total * sizeof(uint4));
     hipLaunchKernelGGL((q4_gemm_xprep_kernel<false>), dim3((unsigned)std::min<size_t>(ceil_div(total, 256), 4096)),
                        dim3(256), 0, m->dev->stream, (const void*)x, (int)w0->cols, (int)w0->cols, (int)w0->Kp,

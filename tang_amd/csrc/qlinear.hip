@@ -139,6 +139,7 @@ static void q4_mfma_launch(const th_qweight* w, const void* x, size_t m, size_t 
         x = xp;
         ldx = w->Kp;
     }
+    TH_REQUIRE(!XP || m * w->Kp * 2 < 0x7FFFFFF0u, "prepared activations above 2 GiB");  // 32-bit buffer offsets
     const size_t NT = w->Np / 16, GQ = w->Kp / 128;
     const unsigned gx = (unsigned)ceil_div(NT, 4 * RT);
     const unsigned gy = (unsigned)ceil_div(m, 16 * CB);

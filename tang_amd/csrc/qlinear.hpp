@@ -10,6 +10,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "ops.hpp"
 
 namespace th {
 
@@ -805,14 +806,19 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
 // partials [KS][m][n] that q4_splitk_reduce sums in a fixed order.
 // ---------------------------------------------------------------------------
 
+// out[k] = f16 pair (element k, element k+4) of the word, each (n-8)*scale.
+// 0x6400|n is exactly 1024+n in f16; byte permutes splice the 0x64 high
+// bytes onto the low / high nibbles of the four bytes (7 integer ops for the
+// word instead of 11 with shifts, masks and ors per pair).
 __device__ __forceinline__ void nib_pairs_f16(uint32_t w, half2_t s2, half2_t out[4]) {
     const half2_t off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const uint32_t lo = w & 0x0F0F0F0Fu;          // bytes: e0 e2 e4 e6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes: e1 e3 e5 e7
+    const uint32_t c64 = 0x64646464u;
+    const uint32_t p[4] = {__builtin_amdgcn_perm(c64, lo, 0x04020400u), __builtin_amdgcn_perm(c64, hi, 0x04020400u),
+                           __builtin_amdgcn_perm(c64, lo, 0x04030401u), __builtin_amdgcn_perm(c64, hi, 0x04030401u)};
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t p = ((w >> (4 * k)) & 0x000F000Fu) | 0x64006400u;
-        half2_t h = __builtin_bit_cast(half2_t, p);
-        out[k] = (h + off) * s2;
-    }
+    for (int k = 0; k < 4; k++) out[k] = (__builtin_bit_cast(half2_t, p[k]) + off) * s2;
 }
 
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
@@ -903,7 +909,9 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
                                                            const void* __restrict__ xin, Epi epi, Src src,
                                                            int N, int K, int Kp, int ldx, int gq_per_split) {
     // LDS B tile: [CB][4 j][4 q][16 col] uint4 (8 f16 each)
-    __shared__ uint4 bt[CB * 4 * 4 * 16];
+    // two B tiles: the next group-quad's is written while this one is read,
+    // so one barrier per step orders both
+    __shared__ uint4 bt2[2][CB * 4 * 4 * 16];
     int mrows = 0;
     {
         const uint4* wsel = wt;
@@ -930,8 +938,9 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
 #pragma unroll
         for (int b = 0; b < CB; b++) acc[a][b] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xin, 0x7FFFFFF0u);  // prepared rows (XP), in-range offsets only
     // staging assignment: CB*16 cols * 16 chunks (4 groups x 4 quads) = CB*256 chunks
-    auto load_x = [&](int gq, uint4 regs[CB]) {
+    auto load_x = [&](int gq, uint4 (&regs)[CB]) {
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             const int idx = tid + i * 256;        // chunk id
@@ -942,10 +951,17 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
             const int ml = cb * 16 + col;
             const int k0 = gq * 128 + j * 32 + qq * 8;
             if constexpr (XP) {  // prepared: f16, permuted, padded (ldx = Kp)
-                regs[i] = ml < mrows ? *(const uint4*)((const uint16_t*)xin + (size_t)src.x_row(ml) * ldx + k0)
-                                     : make_uint4(0, 0, 0, 0);
-                continue;
-            }
+                if constexpr (Src::GROUPED) {  // short work items: skip the loads of empty rows
+                    regs[i] = ml < mrows ? *(const uint4*)((const uint16_t*)xin + (size_t)src.x_row(ml) * ldx + k0)
+                                         : make_uint4(0, 0, 0, 0);
+                } else {
+                    // branch-free: rows past mrows re-read the last live row
+                    // (a finite copy whose D columns are never stored)
+                    const uint32_t off = (uint32_t)(src.x_row(min(ml, mrows - 1)) * ldx + k0) * 2u;
+                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+                    regs[i] = make_uint4(v.x, v.y, v.z, v.w);
+                }
+            } else {
             float xv[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) xv[e] = 0.0f;
@@ -981,9 +997,10 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
             o.z = pack_half2(xv[2], xv[6]);
             o.w = pack_half2(xv[3], xv[7]);
             regs[i] = o;
+            }
         }
     };
-    auto store_x = [&](const uint4 regs[CB]) {
+    auto store_x = [&](uint4* bt, const uint4 (&regs)[CB]) {
 #pragma unroll
         for (int i = 0; i < CB; i++) {
             const int idx = tid + i * 256;
@@ -995,7 +1012,7 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     uint4 xr[CB];
     uint4 wcur[RT], wnxt[RT];
     ScaleVec<RT, ST> scur, snxt;
-    auto load_w = [&](int gq, uint4 w[RT], ScaleVec<RT, ST>& s) {
+    auto load_w = [&](int gq, uint4 (&w)[RT], ScaleVec<RT, ST>& s) {
 #pragma unroll
         for (int a = 0; a < RT; a++) {
             int tt = min(tile0 + a, NT - 1);
@@ -1006,12 +1023,13 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     if (gq0 < gq1) {
         load_x(gq0, xr);
         load_w(gq0, wcur, scur);
+        store_x(bt2[0], xr);
+        __syncthreads();
     }
     for (int gq = gq0; gq < gq1; gq++) {
-        __syncthreads();
-        store_x(xr);
-        __syncthreads();
-        if (gq + 1 < gq1) {
+        const uint4* bt = bt2[(gq - gq0) & 1];
+        const bool more = gq + 1 < gq1;
+        if (more) {
             load_x(gq + 1, xr);
             load_w(gq + 1, wnxt, snxt);
         }
@@ -1034,6 +1052,10 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag[b], acc[a][b], 0, 0, 0);
             }
         }
+        // the other tile was last read in the previous step, before the
+        // barrier that ended it
+        if (more) store_x(bt2[(gq + 1 - gq0) & 1], xr);
+        __syncthreads();
 #pragma unroll
         for (int a = 0; a < RT; a++) wcur[a] = wnxt[a];
         scur = snxt;
