@@ -83,7 +83,23 @@ struct th_device {
     size_t scratch_x_bytes = 0;
     int* counters = nullptr;  // see device_counters
     size_t n_counters = 0;
+    int live = 0;          // buffers, weights and engines that hold this device
+    bool closed = false;   // th_device_destroy ran; the struct waits for live == 0
 };
+
+// Objects holding a th_device keep the struct alive: th_device_destroy
+// drains and releases the stream and workspaces at once, and the struct
+// itself goes with the last object freed after it (so such a free never
+// reads a deleted device).
+inline void device_retain(th_device* d) { d->live++; }
+inline void device_release(th_device* d) {
+    if (--d->live == 0 && d->closed) delete d;
+}
+// Drain the device's stream before freeing memory it may still use (nothing
+// is in flight once the device is closed).
+inline void device_drain(th_device* d) {
+    if (!d->closed) (void)hipStreamSynchronize(d->stream);
+}
 
 struct th_buffer {
     th_device* dev = nullptr;

@@ -131,6 +131,7 @@ th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_d
         delete w;
         throw;
     }
+    device_retain(dev);
     return w;
 }
 
@@ -189,6 +190,7 @@ th_qweight* q8_pack(th_device* dev, const int8_t* q, size_t ldq, const float* sc
         delete w;
         throw;
     }
+    device_retain(dev);
     return w;
 }
 
@@ -234,13 +236,18 @@ int th_device_destroy(th_device* d) {
     if (!d) return TH_OK;
     (void)hipSetDevice(d->ordinal);
     (void)hipStreamSynchronize(d->stream);
+    TH_REQUIRE(!d->closed, "device already destroyed");
     if (d->scratch) (void)hipFree(d->scratch);
     if (d->scratch_x) (void)hipFree(d->scratch_x);
     if (d->counters) (void)hipFree(d->counters);
     (void)hipEventDestroy(d->ev_start);
     (void)hipEventDestroy(d->ev_stop);
     (void)hipStreamDestroy(d->stream);
-    delete d;
+    d->stream = nullptr;
+    d->scratch = d->scratch_x = nullptr;
+    d->counters = nullptr;
+    d->closed = true;
+    if (d->live == 0) delete d;
     TH_API_END
 }
 
@@ -292,6 +299,7 @@ int th_buffer_alloc(th_device* d, th_dtype dt, size_t n, th_buffer** out) {
                         std::string("hipMalloc: ") + hipGetErrorString(e));
         }
     }
+    device_retain(d);
     *out = b;
     TH_API_END
 }
@@ -299,11 +307,13 @@ int th_buffer_alloc(th_device* d, th_dtype dt, size_t n, th_buffer** out) {
 int th_buffer_free(th_buffer* b) {
     TH_API_BEGIN
     if (!b) return TH_OK;
+    th_device* d = b->dev;
     if (b->ptr) {
-        (void)hipStreamSynchronize(b->dev->stream);
-        TH_HIP(hipFree(b->ptr));
+        device_drain(d);
+        (void)hipFree(b->ptr);
     }
     delete b;
+    device_release(d);
     TH_API_END
 }
 
@@ -431,10 +441,12 @@ int th_qweight_info(const th_qweight* w, size_t* rows, size_t* cols, int* bits) 
 int th_qweight_free(th_qweight* w) {
     TH_API_BEGIN
     if (!w) return TH_OK;
-    (void)hipStreamSynchronize(w->dev->stream);
-    if (w->data) TH_HIP(hipFree(w->data));
-    if (w->scales) TH_HIP(hipFree(w->scales));
+    th_device* d = w->dev;
+    device_drain(d);
+    if (w->data) (void)hipFree(w->data);
+    if (w->scales) (void)hipFree(w->scales);
     delete w;
+    device_release(d);
     TH_API_END
 }
 

@@ -385,7 +385,7 @@ namespace th {
 
 static void llama_free(th_llama* m) {
     if (!m) return;
-    (void)hipStreamSynchronize(m->dev->stream);
+    device_drain(m->dev);
     for (auto* v : {&m->wqkv, &m->wo, &m->wgu, &m->wd})
         for (th_qweight* w : *v) th_qweight_free(w);
     if (m->lm) th_qweight_free(m->lm);
@@ -396,7 +396,9 @@ static void llama_free(th_llama* m) {
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    th_device* d = m->dev;
     delete m;
+    device_release(d);
 }
 
 template <typename T>
@@ -606,8 +608,9 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
     TH_REQUIRE(c.d_model <= 4096, "the RMSNorm prologue supports d_model <= 4096");
     TH_REQUIRE(ceil_div((size_t)c.max_seq, (size_t)ATTN_SPLIT_ENGINE) <= 256, "max_seq too long for the attention splits");
     th_llama* m = new th_llama();
+    m->dev = dev;
+    device_retain(dev);
     try {
-        m->dev = dev;
         m->cfg = c;
         m->qd = c.n_heads * c.head_dim;
         m->kvd = c.n_kv_heads * c.head_dim;

@@ -488,7 +488,7 @@ static void moe_reserve(th_moe* m, size_t T) {
 
 static void moe_destroy(th_moe* m) {
     if (!m) return;
-    (void)hipStreamSynchronize(m->dev->stream);
+    device_drain(m->dev);
     for (auto* v : {&m->gu, &m->dn})
         for (th_qweight* w : *v)
             if (w) th_qweight_free(w);
@@ -496,7 +496,9 @@ static void moe_destroy(th_moe* m) {
     for (void* p : ps)
         if (p) (void)hipFree(p);
     moe_free_work(m);
+    th_device* d = m->dev;
     delete m;
+    device_release(d);
 }
 
 template <int MR, typename Epi, int NW>
@@ -562,6 +564,7 @@ int th_moe_create(th_device* dev, size_t d, size_t ff, size_t E, size_t S, size_
     TH_REQUIRE(ff % 8 == 0 && d % 8 == 0, "d and ff must be multiples of 8");
     th_moe* m = new th_moe();
     m->dev = dev; m->d = d; m->ff = ff; m->E = E; m->S = S; m->k = k;
+    device_retain(dev);
     *out = m;
     TH_API_END
 }

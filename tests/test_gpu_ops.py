@@ -128,3 +128,22 @@ def test_convert_roundtrip(dev):
     z = dev.upload(x)
     dev.zero_buffer(z)
     assert not z.to_numpy().any()
+
+
+def test_objects_freed_after_device_close():
+    # Buffers and weights may be freed (explicitly or by the garbage
+    # collector) after their device was destroyed; the free must not read
+    # the destroyed device.
+    d = capi.HipComputeDevice(0)
+    rows, cols = 64, 256
+    nib, sc16 = capi.synth_q4(2, rows, cols)
+    w = d.q4_upload_packed(nib, sc16, rows, cols, capi.F16)
+    x = d.upload(capi.synth_normal(3, cols, 1.0, capi.BF16), capi.BF16)
+    y = d.gemm_q4(x, 1, w)
+    ref = oracle.q4_matvec_soa(nib, oracle.f16_to_f32(sc16), rows, cols,
+                               oracle.bf16_to_f32(capi.synth_normal(3, cols, 1.0, capi.BF16)).astype(np.float64))
+    assert max_abs_rel(y.to_numpy(), ref) < 2e-2
+    d.close()
+    w.free()
+    x.free()
+    del y  # freed by its finaliser, also after the device
