@@ -60,8 +60,8 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
     uint4 hx[NS][ROUTER_TOK];
     float4 wv[NS][EPW][2];
 #pragma unroll
-    for (int st = 0; st < NS; st++) {  // clamped addresses: strides past d re-read the first (not used)
-        const int k0 = (base + st * 512 + lane * 8 < d) ? base + st * 512 + lane * 8 : lane * 8;
+    for (int st = 0; st < NS; st++) {  // clamped addresses: pieces past d re-read the row start (not used)
+        const int k0 = (base + st * 512 + lane * 8 < d) ? base + st * 512 + lane * 8 : 0;
 #pragma unroll
         for (int a = 0; a < ROUTER_TOK; a++)
             hx[st][a] = *(const uint4*)(h + (size_t)min(t0 + a, T - 1) * d + k0);

@@ -45,3 +45,43 @@ def test_moe_small_shape_and_repeat(dev):
             assert max_abs_rel(out, r_out) < 2e-2
     finally:
         capi.lib().th_moe_destroy(m)
+
+
+def test_moe_tied_router_logits(dev):
+    """A zero hidden state gives every expert the same logit: top-k must take
+    experts 0..k-1 in index order (first maximum on ties,
+    sampling.rs:184-194), each with probability 1/E."""
+    cfg = dict(d=256, ff=96, E=8, S=1, k=3)
+    T = 4
+    h = np.zeros(T * cfg["d"], np.uint16)  # bf16 zeros
+    ref = OracleMoe(cfg, 9)
+    r_out, r_idx, r_w = ref.forward(h, T)
+    m = device_moe(dev, cfg, 9)
+    try:
+        out, idx, w = device_moe_forward(dev, m, cfg, h, T)
+    finally:
+        capi.lib().th_moe_destroy(m)
+    expect = np.tile(np.arange(cfg["k"], dtype=np.int32), (T, 1))
+    assert np.array_equal(r_idx, expect) and np.array_equal(idx, expect)
+    assert np.allclose(w, 1.0 / cfg["E"], rtol=0, atol=1e-7)
+    assert max_abs_rel(out, r_out) < 2e-2
+
+
+@pytest.mark.parametrize("T", [20, 70])  # top-k inside the dispatch kernel / in its own kernel
+def test_moe_many_experts(dev, T):
+    """100 routed experts, no shared one: two expert slots per lane in the
+    top-k and a probability row that is not a whole number of 16-float
+    rounds."""
+    cfg = dict(d=256, ff=64, E=100, S=0, k=6)
+    print(f"moe E=100 T={T}", flush=True)
+    h = capi.synth_normal(7 + T, T * cfg["d"], 1.0, capi.BF16)
+    ref = OracleMoe(cfg, 11)
+    r_out, r_idx, r_w = ref.forward(h, T)
+    m = device_moe(dev, cfg, 11)
+    try:
+        out, idx, w = device_moe_forward(dev, m, cfg, h, T)
+    finally:
+        capi.lib().th_moe_destroy(m)
+    assert np.array_equal(idx, r_idx)
+    assert max_abs_rel(w, r_w) < 1e-5
+    assert max_abs_rel(out, r_out) < 2e-2
