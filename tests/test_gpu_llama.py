@@ -37,6 +37,24 @@ def test_small_llama_matches_oracle(dev):
     assert max_abs_rel(logits, r_logits) < 1e-3
 
 
+def test_small_llama_long_context_matches_oracle(dev):
+    """Positions past 4096: more than sixteen 256-position attention splits,
+    so the last split's merge takes a second round of records."""
+    cfg = dict(CONFIG_SMALL, max_seq=4608)
+    seed, kv_seed, prefill, steps = 7, 8, 4400, 8
+    ref = OracleLlama(cfg, seed, kv_seed, prefill)
+    r_toks, margins, r_logits = ref.generate(1, prefill, steps)
+    m = device_llama(dev, cfg, seed, kv_seed, prefill)
+    try:
+        toks, logits = device_generate(m, cfg, 1, prefill, steps)
+    finally:
+        capi.lib().th_llama_destroy(m)
+    print("oracle", r_toks, "min margin %.3e" % min(margins))
+    print("device", list(toks))
+    assert list(toks) == r_toks
+    assert max_abs_rel(logits, r_logits) < 1e-3
+
+
 def test_small_llama_generation_is_resumable(dev):
     """Two generate calls (24 + 24 steps) equal one 48-step call: the KV cache
     and position live on the device (kv_cache.rs:76-100 append semantics)."""
