@@ -31,12 +31,6 @@ __device__ __forceinline__ void st_coherent(float* p, float v) {
 __device__ __forceinline__ void st_coherent(int* p, int v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int ld_coherent(const int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Cache-policy bit of a gfx950 vector memory access that makes it coherent
@@ -50,9 +44,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 }
 
 // Copy n floats that other workgroups stored with st_coherent into LDS.
-// Same coherence as ld_coherent, but plain buffer loads, which the compiler
-// does not serialise (atomic loads each wait for the previous one): sixteen
-// per thread are in flight per round.  Call with the whole 256-thread block.
+// Same coherence as a relaxed agent-scope atomic load, but plain buffer
+// loads, which the compiler does not serialise (atomic loads each wait for
+// the previous one): sixteen per thread are in flight per round.  Call with
+// the whole NT-thread block.
 template <int NT = 256>
 __device__ __forceinline__ void ld_coherent_to_lds(const float* src, int n, float* dst, int tid) {
     const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(src, (uint32_t)n * 4u);
@@ -128,29 +123,6 @@ template <int N>
 __device__ __forceinline__ float tree_sum(const float* r) {
     if constexpr (N == 1) return r[0];
     else return tree_sum<N / 2>(r) + tree_sum<N / 2>(r + N / 2);
-}
-
-// Sum / max over an NT-thread block in a fixed order; every thread gets it.
-template <int NT>
-__device__ __forceinline__ float block_sum_n(float v, float* red) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    return tree_sum<NT / 64>(red);
-}
-template <int NT>
-__device__ __forceinline__ float block_max_n(float v, float* red) {
-    v = wave_max(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float m = red[0];
-#pragma unroll
-    for (int w = 1; w < NT / 64; w++) m = fmaxf(m, red[w]);
-    return m;
 }
 
 // Sum over a 256-thread block; every thread gets the result.
