@@ -215,6 +215,16 @@ int th_llama_destroy(th_llama* m);
 /* Fill all weights with the seeded synthetic generator (th_synth_*): linear
  * tensor t of layer l uses seed th_synth_seed(seed, l, t). */
 int th_llama_init_synthetic(th_llama* m, uint64_t seed);
+/* Replaces load_model (crates/tang-train/examples/smollm.rs:364-420): the
+ * weights of a safetensors file with Llama tensor names
+ * (model.embed_tokens.weight, model.layers.{i}.self_attn.{q,k,v,o}_proj.weight,
+ * model.layers.{i}.mlp.{gate,up,down}_proj.weight,
+ * model.layers.{i}.{input,post_attention}_layernorm.weight, model.norm.weight
+ * and, unless tied to the embedding, lm_head.weight; F64/F32/F16/BF16).
+ * Linears go through quantize_matrix_q4 with f16 block scales, embeddings and
+ * norm weights are stored as bf16.  Every tensor but lm_head is required and
+ * shape-checked (the reference keeps its initial values for a missing one). */
+int th_llama_load_safetensors(th_llama* m, const th_st_file* f);
 /* Fill KV positions [0, len) of every layer with N(0,1) f16 values. */
 int th_llama_fill_kv_synthetic(th_llama* m, size_t len, uint64_t seed);
 /* Greedy decode: feed `token` at position `pos`, then n_steps-1 more steps on

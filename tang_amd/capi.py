@@ -83,6 +83,7 @@ SIGNATURES = {
     "th_llama_create": ([_P, _P, _P], _I),
     "th_llama_destroy": ([_P], _I),
     "th_llama_init_synthetic": ([_P, _U64], _I),
+    "th_llama_load_safetensors": ([_P, _P], _I),
     "th_llama_fill_kv_synthetic": ([_P, _S, _U64], _I),
     "th_llama_generate": ([_P, ctypes.c_int32, _S, _S, _P, _P], _I),
     "th_llama_step_device": ([_P, _S], _I),

@@ -3,6 +3,10 @@
 
 #include "common.hpp"
 
+#include <initializer_list>
+#include <string>
+#include <vector>
+
 // Wrap a C entry point body: exceptions become status codes + last error.
 #define TH_API_BEGIN try {
 #define TH_API_END                                              \
@@ -44,6 +48,11 @@ void require_len_any(const th_buffer* b, size_t n, const char* what);
 
 th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_dtype sdt, size_t rows,
                     size_t cols);
+
+// safetensors helpers (loader.cpp): whether a tensor exists, and a tensor's
+// values as f32 after checking that its shape is exactly `shape`.
+bool st_has(const th_st_file* f, const std::string& name);
+std::vector<float> st_read_shaped(const th_st_file* f, const std::string& name, std::initializer_list<size_t> shape);
 th_qweight* q8_pack(th_device* dev, const int8_t* q, size_t ldq, const float* scales, bool per_row,
                     size_t rows, size_t cols);
 

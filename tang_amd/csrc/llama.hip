@@ -592,6 +592,61 @@ static HostQ4 synth_q4_host(uint64_t seed, size_t rows, size_t cols) {
     return h;
 }
 
+// A row-major f32 matrix through quantize_matrix_q4 (quantize.rs:208-221),
+// with each block's amax/7 scale then rounded to f16, the engine's scale
+// format (relative error <= 2^-11; a nonzero scale outside f16's normal
+// range is rejected rather than flushed).
+static HostQ4 quant_q4_host(const std::vector<float>& w, size_t rows, size_t cols, const std::string& name) {
+    HostQ4 h;
+    h.rows = rows; h.cols = cols;
+    const size_t bpr = ceil_div(cols, (size_t)32);
+    std::vector<th_q4_block> blocks(rows * bpr);
+    check_status(th_quantize_q4(w.data(), rows, cols, blocks.data()));
+    h.nib.resize(rows * bpr * 16);
+    h.sc.resize(rows * bpr);
+    for (size_t i = 0; i < blocks.size(); i++) {
+        std::memcpy(&h.nib[i * 16], blocks[i].values, 16);
+        const float sc = blocks[i].scale;
+        TH_REQUIRE(sc >= 6.103515625e-05f && sc <= 65504.0f, name + ": a block scale is outside the f16 range");
+        h.sc[i] = f32_to_f16_host(sc);
+    }
+    return h;
+}
+
+// Rows of several matrices with the same column count, in order.
+static HostQ4 concat_rows(std::initializer_list<const HostQ4*> parts) {
+    HostQ4 f;
+    f.cols = (*parts.begin())->cols;
+    for (const HostQ4* p : parts) {
+        TH_REQUIRE(p->cols == f.cols, "concatenated matrices differ in width");
+        f.rows += p->rows;
+        f.nib.insert(f.nib.end(), p->nib.begin(), p->nib.end());
+        f.sc.insert(f.sc.end(), p->sc.begin(), p->sc.end());
+    }
+    return f;
+}
+
+// The engine's gate/up matrix: 16-row tile b holds gate rows 8b..8b+7 then
+// up rows 8b..8b+7 (the SwiGLU epilogue pairs them inside one tile).
+static HostQ4 interleave_gate_up(const HostQ4& g, const HostQ4& u) {
+    TH_REQUIRE(g.rows == u.rows && g.cols == u.cols && g.rows % 8 == 0, "gate/up shapes differ");
+    const size_t bpr = ceil_div(g.cols, (size_t)32), ff = g.rows;
+    HostQ4 gi;
+    gi.rows = 2 * ff; gi.cols = g.cols;
+    gi.nib.resize(2 * ff * bpr * 16);
+    gi.sc.resize(2 * ff * bpr);
+    for (size_t b = 0; b < ff / 8; b++) {
+        for (size_t r = 0; r < 8; r++) {
+            const size_t src = 8 * b + r, dg = 16 * b + r, du = 16 * b + 8 + r;
+            std::memcpy(&gi.nib[dg * bpr * 16], &g.nib[src * bpr * 16], bpr * 16);
+            std::memcpy(&gi.nib[du * bpr * 16], &u.nib[src * bpr * 16], bpr * 16);
+            std::memcpy(&gi.sc[dg * bpr], &g.sc[src * bpr], bpr * 2);
+            std::memcpy(&gi.sc[du * bpr], &u.sc[src * bpr], bpr * 2);
+        }
+    }
+    return gi;
+}
+
 }  // namespace th
 
 extern "C" {
@@ -664,40 +719,21 @@ int th_llama_init_synthetic(th_llama* m, uint64_t seed) {
     const th_llama_config& c = m->cfg;
     const size_t d = c.d_model, ff = c.d_ff, L = c.n_layers;
     m->wqkv.assign(L, nullptr); m->wo.assign(L, nullptr); m->wgu.assign(L, nullptr); m->wd.assign(L, nullptr);
-    const size_t bpr_d = ceil_div(d, 32), bpr_ff = ceil_div(ff, 32);
     // Host generation runs in parallel over layers; uploads stay serial.
     std::vector<HostQ4> qkv(L), wo(L), gu(L), dn(L);
     std::string err;
 #pragma omp parallel for schedule(dynamic, 1)
     for (long l = 0; l < (long)L; l++) {
         try {
-            HostQ4 q = synth_q4_host(th_synth_seed(seed, l, T_WQ), m->qd, d);
-            HostQ4 k = synth_q4_host(th_synth_seed(seed, l, T_WK), m->kvd, d);
-            HostQ4 v = synth_q4_host(th_synth_seed(seed, l, T_WV), m->kvd, d);
-            HostQ4& f = qkv[l];
-            f.rows = q.rows + k.rows + v.rows; f.cols = d;
-            f.nib = std::move(q.nib); f.nib.insert(f.nib.end(), k.nib.begin(), k.nib.end());
-            f.nib.insert(f.nib.end(), v.nib.begin(), v.nib.end());
-            f.sc = std::move(q.sc); f.sc.insert(f.sc.end(), k.sc.begin(), k.sc.end());
-            f.sc.insert(f.sc.end(), v.sc.begin(), v.sc.end());
+            const HostQ4 q = synth_q4_host(th_synth_seed(seed, l, T_WQ), m->qd, d);
+            const HostQ4 k = synth_q4_host(th_synth_seed(seed, l, T_WK), m->kvd, d);
+            const HostQ4 v = synth_q4_host(th_synth_seed(seed, l, T_WV), m->kvd, d);
+            qkv[l] = concat_rows({&q, &k, &v});
             wo[l] = synth_q4_host(th_synth_seed(seed, l, T_WO), d, d);
-            HostQ4 g = synth_q4_host(th_synth_seed(seed, l, T_WG), ff, d);
-            HostQ4 u = synth_q4_host(th_synth_seed(seed, l, T_WU), ff, d);
-            HostQ4& gi = gu[l];
-            gi.rows = 2 * ff; gi.cols = d;
-            gi.nib.resize(2 * ff * bpr_d * 16);
-            gi.sc.resize(2 * ff * bpr_d);
-            for (size_t b = 0; b < ff / 8; b++) {
-                for (size_t r = 0; r < 8; r++) {
-                    const size_t src = 8 * b + r, dg = 16 * b + r, du = 16 * b + 8 + r;
-                    std::memcpy(&gi.nib[dg * bpr_d * 16], &g.nib[src * bpr_d * 16], bpr_d * 16);
-                    std::memcpy(&gi.nib[du * bpr_d * 16], &u.nib[src * bpr_d * 16], bpr_d * 16);
-                    std::memcpy(&gi.sc[dg * bpr_d], &g.sc[src * bpr_d], bpr_d * 2);
-                    std::memcpy(&gi.sc[du * bpr_d], &u.sc[src * bpr_d], bpr_d * 2);
-                }
-            }
+            const HostQ4 g = synth_q4_host(th_synth_seed(seed, l, T_WG), ff, d);
+            const HostQ4 u = synth_q4_host(th_synth_seed(seed, l, T_WU), ff, d);
+            gu[l] = interleave_gate_up(g, u);
             dn[l] = synth_q4_host(th_synth_seed(seed, l, T_WD), d, ff);
-            (void)bpr_ff;
         } catch (const std::exception& e) {
 #pragma omp critical
             err = e.what();
@@ -725,6 +761,71 @@ int th_llama_init_synthetic(th_llama* m, uint64_t seed) {
         TH_HIP(hipMemcpy(m->ffn_norm + l * d, buf.data(), d * 2, hipMemcpyHostToDevice));
     }
     check_status(th_synth_normal(th_synth_seed(seed, L, T_FINAL_NORM), d, NORM_STD, TH_BF16, buf.data()));
+    TH_HIP(hipMemcpy(m->final_norm, buf.data(), d * 2, hipMemcpyHostToDevice));
+    m->weights_ready = true;
+    TH_API_END
+}
+
+int th_llama_load_safetensors(th_llama* m, const th_st_file* f) {
+    TH_API_BEGIN
+    TH_REQUIRE(m && f, "null argument");
+    TH_REQUIRE(!m->weights_ready, "weights already initialised");
+    const th_llama_config& c = m->cfg;
+    const size_t d = c.d_model, ff = c.d_ff, L = c.n_layers, V = c.vocab;
+    // smollm.rs:364-420 (load_model), with every tensor required except
+    // lm_head.weight, which falls back to the embedding (weight tying)
+    std::vector<HostQ4> qkv(L), wo(L), gu(L), dn(L);
+    std::vector<uint16_t> attn_norm(L * d), ffn_norm(L * d);
+    std::string err;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long l = 0; l < (long)L; l++) {
+        try {
+            const std::string pre = "model.layers." + std::to_string(l) + ".";
+            auto lin = [&](const char* name, size_t rows, size_t cols) {
+                const std::string n = pre + name;
+                return quant_q4_host(st_read_shaped(f, n, {rows, cols}), rows, cols, n);
+            };
+            const HostQ4 q = lin("self_attn.q_proj.weight", m->qd, d);
+            const HostQ4 k = lin("self_attn.k_proj.weight", m->kvd, d);
+            const HostQ4 v = lin("self_attn.v_proj.weight", m->kvd, d);
+            qkv[l] = concat_rows({&q, &k, &v});
+            wo[l] = lin("self_attn.o_proj.weight", d, m->qd);
+            const HostQ4 g = lin("mlp.gate_proj.weight", ff, d);
+            const HostQ4 u = lin("mlp.up_proj.weight", ff, d);
+            gu[l] = interleave_gate_up(g, u);
+            dn[l] = lin("mlp.down_proj.weight", d, ff);
+            const std::vector<float> an = st_read_shaped(f, pre + "input_layernorm.weight", {d});
+            const std::vector<float> fn = st_read_shaped(f, pre + "post_attention_layernorm.weight", {d});
+            for (size_t i = 0; i < d; i++) {
+                attn_norm[l * d + i] = f32_to_bf16_host(an[i]);
+                ffn_norm[l * d + i] = f32_to_bf16_host(fn[i]);
+            }
+        } catch (const std::exception& e) {
+#pragma omp critical
+            err = e.what();
+        }
+    }
+    if (!err.empty()) throw Error(TH_ERR_INVALID, err);
+    const std::vector<float> emb = st_read_shaped(f, "model.embed_tokens.weight", {V, d});
+    const std::vector<float> fin = st_read_shaped(f, "model.norm.weight", {d});
+    HostQ4 lm = st_has(f, "lm_head.weight")
+                    ? quant_q4_host(st_read_shaped(f, "lm_head.weight", {V, d}), V, d, "lm_head.weight")
+                    : quant_q4_host(emb, V, d, "model.embed_tokens.weight (tied lm_head)");
+    m->wqkv.assign(L, nullptr); m->wo.assign(L, nullptr); m->wgu.assign(L, nullptr); m->wd.assign(L, nullptr);
+    for (size_t l = 0; l < L; l++) {
+        m->wqkv[l] = q4_pack(m->dev, qkv[l].nib.data(), qkv[l].sc.data(), TH_F16, qkv[l].rows, d);
+        m->wo[l] = q4_pack(m->dev, wo[l].nib.data(), wo[l].sc.data(), TH_F16, d, m->qd);
+        m->wgu[l] = q4_pack(m->dev, gu[l].nib.data(), gu[l].sc.data(), TH_F16, 2 * ff, d);
+        m->wd[l] = q4_pack(m->dev, dn[l].nib.data(), dn[l].sc.data(), TH_F16, d, ff);
+        qkv[l] = HostQ4(); wo[l] = HostQ4(); gu[l] = HostQ4(); dn[l] = HostQ4();
+    }
+    m->lm = q4_pack(m->dev, lm.nib.data(), lm.sc.data(), TH_F16, V, d);
+    std::vector<uint16_t> buf(V * d);
+    for (size_t i = 0; i < buf.size(); i++) buf[i] = f32_to_bf16_host(emb[i]);
+    TH_HIP(hipMemcpy(m->embed, buf.data(), buf.size() * 2, hipMemcpyHostToDevice));
+    TH_HIP(hipMemcpy(m->attn_norm, attn_norm.data(), L * d * 2, hipMemcpyHostToDevice));
+    TH_HIP(hipMemcpy(m->ffn_norm, ffn_norm.data(), L * d * 2, hipMemcpyHostToDevice));
+    for (size_t i = 0; i < d; i++) buf[i] = f32_to_bf16_host(fin[i]);
     TH_HIP(hipMemcpy(m->final_norm, buf.data(), d * 2, hipMemcpyHostToDevice));
     m->weights_ready = true;
     TH_API_END

@@ -170,6 +170,22 @@ static std::vector<float> st_read(const th_st_file* f, const StTensor& t) {
     return out;
 }
 
+namespace th {
+
+bool st_has(const th_st_file* f, const std::string& name) {
+    for (const StTensor& t : f->tensors)
+        if (t.name == name) return true;
+    return false;
+}
+
+std::vector<float> st_read_shaped(const th_st_file* f, const std::string& name, std::initializer_list<size_t> shape) {
+    const StTensor& t = st_find(f, name.c_str());
+    TH_REQUIRE(t.shape == std::vector<size_t>(shape), "safetensors: " + name + " has an unexpected shape");
+    return st_read(f, t);
+}
+
+}  // namespace th
+
 extern "C" {
 
 int th_quantize_q4(const float* data, size_t rows, size_t cols, th_q4_block* out) {

@@ -28,8 +28,24 @@ def _q4(seed, rows, cols):
     return nib, oracle.f16_to_f32(sc16)
 
 
+def _q4_from_f32(w, rows, cols):
+    """quantize_matrix_q4 (quantize.rs:208-221), block scales rounded to f16
+    as the engine stores them."""
+    blocks = oracle.quantize_matrix_q4(np.ascontiguousarray(w, np.float32).reshape(-1), rows, cols)
+    nib = np.ascontiguousarray(blocks["values"]).reshape(-1)
+    return nib, oracle.f16_to_f32(oracle.f32_to_f16(blocks["scale"]))
+
+
+LINEAR_NAMES = {"wq": "self_attn.q_proj", "wk": "self_attn.k_proj", "wv": "self_attn.v_proj",
+                "wo": "self_attn.o_proj", "wg": "mlp.gate_proj", "wu": "mlp.up_proj", "wd": "mlp.down_proj"}
+
+
 class OracleLlama:
-    def __init__(self, cfg, seed, kv_seed, prefill_len):
+    """Seeded synthetic weights (as th_llama_init_synthetic), or with
+    `tensors` (Llama tensor name -> f32 array) the weights a safetensors
+    file gives th_llama_load_safetensors."""
+
+    def __init__(self, cfg, seed, kv_seed, prefill_len, tensors=None):
         self.cfg = cfg
         c = cfg
         L, d, ff = c["n_layers"], c["d_model"], c["d_ff"]
@@ -40,17 +56,30 @@ class OracleLlama:
                   "wg": (T_WG, ff, d), "wu": (T_WU, ff, d), "wd": (T_WD, d, ff)}
         for l in range(L):
             for name, (tid, rows, cols) in shapes.items():
-                nib, sc = _q4(capi.synth_seed(seed, l, tid), rows, cols)
+                if tensors is None:
+                    nib, sc = _q4(capi.synth_seed(seed, l, tid), rows, cols)
+                else:
+                    nib, sc = _q4_from_f32(tensors["model.layers.%d.%s.weight" % (l, LINEAR_NAMES[name])], rows, cols)
                 self.keep += [nib, sc]
                 views[name][l] = oracle.Q4View(oracle.p(nib), oracle.p(sc))
-        lm_nib, lm_sc = _q4(capi.synth_seed(seed, L, T_LM_HEAD), c["vocab"], d)
+        if tensors is None:
+            lm_nib, lm_sc = _q4(capi.synth_seed(seed, L, T_LM_HEAD), c["vocab"], d)
+            self.embed = capi.synth_normal(capi.synth_seed(seed, L, T_EMBED), c["vocab"] * d, NORM_STD, capi.BF16)
+            self.attn_norm = np.concatenate([capi.synth_normal(capi.synth_seed(seed, l, T_ATTN_NORM), d, NORM_STD,
+                                                               capi.BF16) for l in range(L)])
+            self.ffn_norm = np.concatenate([capi.synth_normal(capi.synth_seed(seed, l, T_FFN_NORM), d, NORM_STD,
+                                                              capi.BF16) for l in range(L)])
+            self.final_norm = capi.synth_normal(capi.synth_seed(seed, L, T_FINAL_NORM), d, NORM_STD, capi.BF16)
+        else:
+            emb = tensors["model.embed_tokens.weight"]
+            lm_nib, lm_sc = _q4_from_f32(tensors.get("lm_head.weight", emb), c["vocab"], d)
+            self.embed = oracle.f32_to_bf16(emb.reshape(-1))
+            self.attn_norm = np.concatenate([oracle.f32_to_bf16(tensors["model.layers.%d.input_layernorm.weight" % l])
+                                             for l in range(L)])
+            self.ffn_norm = np.concatenate([oracle.f32_to_bf16(
+                tensors["model.layers.%d.post_attention_layernorm.weight" % l]) for l in range(L)])
+            self.final_norm = oracle.f32_to_bf16(tensors["model.norm.weight"])
         self.keep += [lm_nib, lm_sc]
-        self.embed = capi.synth_normal(capi.synth_seed(seed, L, T_EMBED), c["vocab"] * d, NORM_STD, capi.BF16)
-        self.attn_norm = np.concatenate([capi.synth_normal(capi.synth_seed(seed, l, T_ATTN_NORM), d, NORM_STD,
-                                                           capi.BF16) for l in range(L)])
-        self.ffn_norm = np.concatenate([capi.synth_normal(capi.synth_seed(seed, l, T_FFN_NORM), d, NORM_STD,
-                                                          capi.BF16) for l in range(L)])
-        self.final_norm = capi.synth_normal(capi.synth_seed(seed, L, T_FINAL_NORM), d, NORM_STD, capi.BF16)
         self.cos, self.sin = oracle.rope_tables(c["head_dim"], c["max_seq"], c["rope_theta"])
         self.kc = np.zeros((L, c["max_seq"], kvd), np.uint16)
         self.vc = np.zeros((L, c["max_seq"], kvd), np.uint16)

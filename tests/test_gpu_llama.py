@@ -252,3 +252,76 @@ def test_small_llama_prefill_matches_oracle(dev, n, hd):
     assert err < 2e-2
     assert nxt == int(r_next)
     assert list(cont) == r_cont
+
+
+@pytest.mark.parametrize("tied", [False, True])
+def test_llama_from_safetensors_matches_oracle(dev, tmp_path, tied):
+    """th_llama_load_safetensors (load_model, smollm.rs:364-420) on a small
+    random model written with the safetensors package: f32 tensors, one f16
+    tensor, and with `tied` no lm_head.weight (the embedding is reused).
+    The oracle quantizes the same values with quantize_matrix_q4."""
+    from safetensors.numpy import save_file
+
+    cfg = CONFIG_SMALL
+    L, d, ff, V = cfg["n_layers"], cfg["d_model"], cfg["d_ff"], cfg["vocab"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    rng = np.random.default_rng(5 + tied)
+    shapes = {"self_attn.q_proj": (qd, d), "self_attn.k_proj": (kvd, d), "self_attn.v_proj": (kvd, d),
+              "self_attn.o_proj": (d, qd), "mlp.gate_proj": (ff, d), "mlp.up_proj": (ff, d),
+              "mlp.down_proj": (d, ff)}
+    # a tied head reads the embedding: keep it small, or every step repeats the input token
+    stored = {"model.embed_tokens.weight": rng.normal(0, 0.02 if tied else 0.5, (V, d)).astype(np.float32),
+              "model.norm.weight": rng.normal(1, 0.1, d).astype(np.float32)}
+    if not tied:
+        stored["lm_head.weight"] = rng.normal(0, 0.05, (V, d)).astype(np.float32)
+    for l in range(L):
+        for name, shape in shapes.items():
+            stored["model.layers.%d.%s.weight" % (l, name)] = rng.normal(0, 0.05, shape).astype(np.float32)
+        stored["model.layers.%d.input_layernorm.weight" % l] = rng.normal(1, 0.1, d).astype(np.float32)
+        stored["model.layers.%d.post_attention_layernorm.weight" % l] = rng.normal(1, 0.1, d).astype(np.float32)
+    stored["model.layers.0.self_attn.q_proj.weight"] = stored["model.layers.0.self_attn.q_proj.weight"].astype(
+        np.float16)
+    path = tmp_path / "model.safetensors"
+    save_file(stored, str(path))
+    tensors = {k: v.astype(np.float32) for k, v in stored.items()}
+
+    prefill, steps = 60, 24
+    ref = OracleLlama(cfg, 0, 8, prefill, tensors=tensors)
+    r_toks, margins, r_logits = ref.generate(1, prefill, steps)
+    c = capi.LlamaConfig(L, d, cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], ff, V, cfg["max_seq"],
+                         cfg["eps"], cfg["rope_theta"])
+    m = ctypes.c_void_p()
+    f = capi.SafetensorsFile(path)
+    capi.check(capi.lib().th_llama_create(dev.handle, ctypes.byref(c), ctypes.byref(m)))
+    try:
+        capi.check(capi.lib().th_llama_load_safetensors(m, f.handle))
+        capi.check(capi.lib().th_llama_fill_kv_synthetic(m, prefill, 8))
+        toks, logits = device_generate(m, cfg, 1, prefill, steps)
+    finally:
+        capi.lib().th_llama_destroy(m)
+        f.close()
+    print("oracle", r_toks[:12], "min margin %.3e" % min(margins))
+    print("device", list(toks[:12]))
+    assert list(toks) == r_toks
+    # bf16 activations: with O(1) norm weights a one-ulp bf16 difference at a
+    # rounding point moves the logits by ~1e-3, so the bf16 bound applies
+    assert max_abs_rel(logits, r_logits) < 2e-2
+
+
+def test_llama_safetensors_rejects_missing_and_misshaped(dev, tmp_path):
+    from safetensors.numpy import save_file
+
+    cfg = CONFIG_SMALL
+    c = capi.LlamaConfig(cfg["n_layers"], cfg["d_model"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"],
+                         cfg["d_ff"], cfg["vocab"], cfg["max_seq"], cfg["eps"], cfg["rope_theta"])
+    path = tmp_path / "bad.safetensors"
+    save_file({"model.embed_tokens.weight": np.zeros((3, 5), np.float32)}, str(path))
+    f = capi.SafetensorsFile(path)
+    m = ctypes.c_void_p()
+    capi.check(capi.lib().th_llama_create(dev.handle, ctypes.byref(c), ctypes.byref(m)))
+    try:
+        with pytest.raises(capi.TangHipError):
+            capi.check(capi.lib().th_llama_load_safetensors(m, f.handle))
+    finally:
+        capi.lib().th_llama_destroy(m)
+        f.close()
