@@ -1,4 +1,4 @@
-// MLA (multi-head latent attention) decode, absorbed form.
+// MLA (multi-head latent attention) decode, absorbed form (DeepSeek-V2-Lite shape: 16 heads, latent 512, rope 64).
 // The reference has no MLA; this is the definition of DeepSeek-V2's absorbed
 // decode with the reference's kv_attention semantics (cpu.rs:257: softmax of
 // scaled scores over every cached position, f32 accumulation):

@@ -1,4 +1,4 @@
-// DeepSeek-style MoE FFN layer with int4 group-32 experts.
+// DeepSeek-style MoE FFN layer with int4 group-32 experts (benchmark shape: d 2048, ff 1408, 64 + 2 experts, top-6).
 // The reference has no MoE; the layer is composed from its ops:
 //   logits = h . W_r^T, p = softmax(logits) (cpu.rs:105-124), the top-k
 //   experts by p (first maximum wins, as sampling.rs:184's argmax), weights

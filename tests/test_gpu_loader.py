@@ -1,4 +1,4 @@
-"""Safetensors weights into the device layout (SURVEY next item 2): a bf16
+"""Safetensors weights into the device layout: a bf16
 matrix quantized on upload (quantize_matrix_q4, quantize.rs:208) comes back
 bit-exact through th_q4_download_blocks and multiplies like the oracle's
 q4_matvec; plain tensors land as f32 / bf16 / f16 device buffers."""

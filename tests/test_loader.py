@@ -1,4 +1,4 @@
-"""Weight loading (SURVEY next item 2): the product quantizers
+"""Weight loading: the product quantizers
 (quantize_matrix_q4/q8, quantize.rs:193-220) against the oracle restatement,
 and the safetensors reader against files written by the `safetensors`
 package (the format tang-safetensors reads, crates/tang-safetensors/src/lib.rs:11-70).
