@@ -159,7 +159,10 @@ int th_gemv_q8(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w
  * through the n_w weights (all of one shape) so the streamed bytes exceed the
  * last-level cache, and return the elapsed milliseconds between HIP events
  * recorded on the device stream around them.  use_graph != 0 captures the
- * calls into one HIP graph first and times its replay. */
+ * calls into one HIP graph first and times its replay.  Launch i reads weight
+ * ws[i % n_w], and the untimed warm-up ends with one pass over ws[0..n_w) in
+ * that order, so every timed launch's weights were last read n_w launches
+ * earlier, for any iters. */
 int th_bench_linear(th_device* dev, const th_buffer* x, size_t m, th_qweight* const* ws, size_t n_w,
                     th_buffer* y, size_t iters, int use_graph, float* ms);
 

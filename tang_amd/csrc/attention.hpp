@@ -194,7 +194,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
                                                            const _Float16* __restrict__ kc,
                                                            const _Float16* __restrict__ vc, int n_heads,
                                                            int n_kv_heads, int pos0, int n,
-                                                           uint16_t* __restrict__ out, int ldo) {
+                                                           uint16_t* __restrict__ out, int ldo,
+                                                           int* __restrict__ xexp) {
     constexpr int KB = 64;          // keys per block
     constexpr int KS = D + 8;       // Ks row stride (halves)
     constexpr int VS = KB + 8;      // Vt row stride (halves)
@@ -337,7 +338,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
     const float inv = 1.0f / l_run;
     if constexpr (XP) {
         // the O projection's prepared layout: the 8-dim chunk of lane groups
-        // g (even) and g+1 goes out from the even lane as (x0,x4,x1,x5,...)
+        // g (even) and g+1 goes out from the even lane as (x0,x4,x1,x5,...).
+        // Row exponent 0: an output row averages V rows of the f16 cache, so
+        // it stays within f16's range.
+        if (h == 0 && g == 0 && qi < n) xexp[qi] = 0;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             float y[4], z[4];
@@ -364,17 +368,18 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float* __restri
 }
 
 // out: bf16 rows of ldo, or (xp) the MFMA GEMM's prepared f16 layout (rows
-// of ldo >= n_heads * head_dim, which must then be the consumer's Kp).
+// of ldo >= n_heads * head_dim, which must then be the consumer's Kp) with
+// row exponents xexp.
 inline void launch_attn_prefill(const float* q, int ldq, const _Float16* kc, const _Float16* vc, int n_heads,
                                 int n_kv_heads, int head_dim, int pos0, int n, uint16_t* out, int ldo, bool xp,
-                                hipStream_t s) {
+                                int* xexp, hipStream_t s) {
     TH_REQUIRE(n >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0, "prefill attention: bad shape");
     const dim3 grid((unsigned)ceil_div((size_t)n, (size_t)64), (unsigned)n_heads);
     switch (head_dim * 2 + (xp ? 1 : 0)) {
-        case 128: hipLaunchKernelGGL((attn_prefill_kernel<64, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
-        case 129: hipLaunchKernelGGL((attn_prefill_kernel<64, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
-        case 256: hipLaunchKernelGGL((attn_prefill_kernel<128, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
-        case 257: hipLaunchKernelGGL((attn_prefill_kernel<128, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo); break;
+        case 128: hipLaunchKernelGGL((attn_prefill_kernel<64, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
+        case 129: hipLaunchKernelGGL((attn_prefill_kernel<64, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
+        case 256: hipLaunchKernelGGL((attn_prefill_kernel<128, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
+        case 257: hipLaunchKernelGGL((attn_prefill_kernel<128, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
         default: throw Error(TH_ERR_INVALID, "prefill attention: head_dim must be 64 or 128");
     }
     TH_LAUNCH_CHECK();

@@ -58,12 +58,21 @@ th_qweight* q8_pack(th_device* dev, const int8_t* q, size_t ldq, const float* sc
 
 // Quantized linear launchers (qlinear.hip).  x: [m][ldx] f32 or bf16,
 // y: [m][ldy] f32.
-// The MFMA GEMM on activations already in its prepared layout: f16 rows of
-// w->Kp (zero past K), each 8-value chunk ordered x0,x4,x1,x5,x2,x6,x3,x7.
-// For producers that can write that layout directly; m > 16.  accumulate:
-// y += x.W^T (a fused residual add) instead of y = x.W^T.
-void launch_q4_linear_prepared(const th_qweight* w, const uint16_t* xp, size_t m, float* y, size_t ldy,
-                               hipStream_t s, th_device* dev, bool accumulate = false);
+// Activations in the MFMA GEMM's prepared layout: row r holds the f16 values
+// x[r][k] * 2^-xexp[r] in rows of the weight's Kp (zero past K), each 8-value
+// chunk ordered x0,x4,x1,x5,x2,x6,x3,x7.
+struct PreparedX {
+    const uint16_t* x;
+    const int* xexp;
+};
+// prepare_x writes that layout for m rows of x (input row rows[r] for output
+// row r when rows is set) into the device's operand workspace.
+PreparedX prepare_x(th_device* dev, const void* x, bool xf32, size_t m, size_t ldx, size_t K, size_t Kp,
+                    hipStream_t s, const int* rows = nullptr);
+// The MFMA GEMM on prepared activations, for producers that write the layout
+// directly.  accumulate: y += x.W^T (a fused residual add) instead of y = x.W^T.
+void launch_q4_linear_prepared(const th_qweight* w, PreparedX xp, size_t m, float* y, size_t ldy, hipStream_t s,
+                               th_device* dev, bool accumulate = false);
 void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
                       size_t ldy, hipStream_t stream, th_device* dev);
 void launch_q8_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,

@@ -130,4 +130,5 @@ struct th_qweight {
     void* data = nullptr;    // packed tiles
     void* scales = nullptr;
     size_t data_bytes = 0, scale_bytes = 0;
+    int* row_exp = nullptr;  // q4: [Np] power-of-two exponent of each row's largest scale (MFMA GEMM)
 };

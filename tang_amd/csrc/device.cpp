@@ -5,6 +5,7 @@
 // one HIP stream per device (the reference CUDA backend also uses a single
 // stream, crates/tang-compute/src/cuda.rs:155-158).
 #include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <vector>
 
@@ -116,6 +117,20 @@ th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_d
             std::memcpy(stile.data() + q4_scale_index(f16, t, gq, rr, j, GQ) * ssz, s, ssz);
         }
     }
+    // per-row scale exponents for the MFMA GEMM's f16 operands (row maximum
+    // scale brought to [2^8, 2^9); padding rows 0)
+    std::vector<int> rexp(Np, 0);
+    for (size_t row = 0; row < rows; row++) {
+        float mx = 0.0f;
+        for (size_t g = 0; g < bpr; g++) {
+            const uint8_t* sp = (const uint8_t*)scales + (row * bpr + g) * ssz;
+            float v;
+            if (f16) { uint16_t h; std::memcpy(&h, sp, 2); v = f16_to_f32_host(h); }
+            else std::memcpy(&v, sp, 4);
+            mx = std::max(mx, std::fabs(v));
+        }
+        rexp[row] = range_exp(mx, WSCALE_TOP);
+    }
     th_qweight* w = new th_qweight();
     w->dev = dev; w->bits = 4; w->rows = rows; w->cols = cols; w->Np = Np; w->Kp = Kp;
     w->scale_dtype = sdt;
@@ -123,11 +138,14 @@ th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_d
     try {
         TH_HIP(hipMalloc(&w->data, w->data_bytes));
         TH_HIP(hipMalloc(&w->scales, w->scale_bytes));
+        TH_HIP(hipMalloc(&w->row_exp, Np * sizeof(int)));
         TH_HIP(hipMemcpy(w->data, tiles.data(), w->data_bytes, hipMemcpyHostToDevice));
         TH_HIP(hipMemcpy(w->scales, stile.data(), w->scale_bytes, hipMemcpyHostToDevice));
+        TH_HIP(hipMemcpy(w->row_exp, rexp.data(), Np * sizeof(int), hipMemcpyHostToDevice));
     } catch (...) {
         if (w->data) (void)hipFree(w->data);
         if (w->scales) (void)hipFree(w->scales);
+        if (w->row_exp) (void)hipFree(w->row_exp);
         delete w;
         throw;
     }
@@ -445,6 +463,7 @@ int th_qweight_free(th_qweight* w) {
     device_drain(d);
     if (w->data) (void)hipFree(w->data);
     if (w->scales) (void)hipFree(w->scales);
+    if (w->row_exp) (void)hipFree(w->row_exp);
     delete w;
     device_release(d);
     TH_API_END

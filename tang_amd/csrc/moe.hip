@@ -339,14 +339,17 @@ struct MoeGemmSrc {
     const MoeWork* work;
     const uint4* const* wdata;
     const _Float16* const* wscales;
+    const int* const* wexps;  // per-expert th_qweight::row_exp
     const int* slot_token;  // null: activation rows are the slots themselves
     int slot0 = 0;
     template <typename ST>
-    __device__ __forceinline__ bool select(int by, int, const uint4*& wt, const ST*& sc, int& mrows) {
+    __device__ __forceinline__ bool select(int by, int, const uint4*& wt, const ST*& sc, const int*& wexp,
+                                           int& mrows) {
         const MoeWork w = work[by];
         if (w.expert < 0) return false;
         wt = wdata[w.expert];
         sc = (const ST*)wscales[w.expert];
+        wexp = wexps[w.expert];
         mrows = w.rows;
         slot0 = w.slot0;
         return true;
@@ -443,6 +446,8 @@ struct th_moe {
     const _Float16** gu_scales = nullptr;
     const uint4** dn_data = nullptr;
     const _Float16** dn_scales = nullptr;
+    const int** gu_exps = nullptr;
+    const int** dn_exps = nullptr;
     size_t T_cap = 0;
     int *offsets = nullptr, *slot_token = nullptr, *token_slot = nullptr;
     MoeWork* work = nullptr;
@@ -492,7 +497,8 @@ static void moe_destroy(th_moe* m) {
     for (auto* v : {&m->gu, &m->dn})
         for (th_qweight* w : *v)
             if (w) th_qweight_free(w);
-    void* ps[] = {m->router, (void*)m->gu_data, (void*)m->gu_scales, (void*)m->dn_data, (void*)m->dn_scales};
+    void* ps[] = {m->router,         (void*)m->gu_data, (void*)m->gu_scales, (void*)m->dn_data,
+                  (void*)m->dn_scales, (void*)m->gu_exps, (void*)m->dn_exps};
     for (void* p : ps)
         if (p) (void)hipFree(p);
     moe_free_work(m);
@@ -533,22 +539,16 @@ constexpr int MOE_GEMM_CB = 4;  // 16-slot blocks per work item (64 slots)
 
 template <typename Epi>
 static void moe_grouped_gemm(const th_moe* m, const th_qweight* w0, const uint4* const* data,
-                             const _Float16* const* scales, const uint16_t* x, size_t x_rows, const int* slot_token,
-                             size_t max_work, Epi epi) {
-    // the x_rows activation rows (tokens, or slots) converted to f16 once
-    const size_t total = x_rows * (w0->Kp / 8);
-    TH_REQUIRE(total * sizeof(uint4) < 0x7FFFFFF0u, "prepared activations above 2 GiB");  // 32-bit buffer offsets
-    uint4* xp = (uint4*)device_scratch_x(m->dev, total * sizeof(uint4));
-    hipLaunchKernelGGL((q4_gemm_xprep_kernel<false>), dim3((unsigned)std::min<size_t>(ceil_div(total, 256), 4096)),
-                       dim3(256), 0, m->dev->stream, (const void*)x, (int)w0->cols, (int)w0->cols, (int)w0->Kp,
-                       (int)x_rows, xp);
-    TH_LAUNCH_CHECK();
-    MoeGemmSrc src{m->work, data, scales, slot_token};
+                             const _Float16* const* scales, const int* const* wexps, const uint16_t* x, size_t x_rows,
+                             const int* slot_token, size_t max_work, Epi epi) {
+    // the x_rows activation rows (tokens, or slots) prepared once
+    const PreparedX xp = prepare_x(m->dev, x, false, x_rows, w0->cols, w0->cols, w0->Kp, m->dev->stream);
+    MoeGemmSrc src{m->work, data, scales, wexps, slot_token};
     const unsigned gx = (unsigned)ceil_div(w0->Np / 16, (size_t)(4 * MOE_GEMM_RT));
-    hipLaunchKernelGGL((q4_gemm_mfma_kernel<MOE_GEMM_RT, MOE_GEMM_CB, false, _Float16, MoeGemmSrc, Epi, true>),
+    hipLaunchKernelGGL((q4_gemm_mfma_kernel<MOE_GEMM_RT, MOE_GEMM_CB, _Float16, MoeGemmSrc, Epi>),
                        dim3(gx, (unsigned)max_work, 1), dim3(256), 0, m->dev->stream, (const uint4*)nullptr,
-                       (const _Float16*)nullptr, (const void*)xp, epi, src, (int)w0->rows, (int)w0->cols,
-                       (int)w0->Kp, (int)w0->Kp, (int)(w0->Kp / 128));
+                       (const _Float16*)nullptr, (const int*)nullptr, xp.x, xp.xexp, epi, src, (int)w0->rows,
+                       (int)w0->cols, (int)w0->Kp, (int)w0->Kp, (int)(w0->Kp / 128));
     TH_LAUNCH_CHECK();
 }
 
@@ -615,6 +615,8 @@ int th_moe_init_synthetic(th_moe* m, uint64_t seed) {
     table((const void**&)m->gu_scales, [&](size_t e) { return (const void*)m->gu[e]->scales; });
     table((const void**&)m->dn_data, [&](size_t e) { return (const void*)m->dn[e]->data; });
     table((const void**&)m->dn_scales, [&](size_t e) { return (const void*)m->dn[e]->scales; });
+    table((const void**&)m->gu_exps, [&](size_t e) { return (const void*)m->gu[e]->row_exp; });
+    table((const void**&)m->dn_exps, [&](size_t e) { return (const void*)m->dn[e]->row_exp; });
     m->ready = true;
     TH_API_END
 }
@@ -654,9 +656,10 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
         moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeStore, 4>(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, nullptr,
                                                        max_work, EpiMoeStore{{}, m->ybuf, (int)m->d});
     } else {
-        moe_grouped_gemm(m, m->gu[0], m->gu_data, m->gu_scales, hx, T, m->slot_token, max_work,
+        moe_grouped_gemm(m, m->gu[0], m->gu_data, m->gu_scales, m->gu_exps, hx, T, m->slot_token, max_work,
                          EpiGemmMoeSwiGLU{m->hbuf, (int)m->ff});
-        moe_grouped_gemm(m, m->dn[0], m->dn_data, m->dn_scales, m->hbuf, T * (m->k + m->S), nullptr, max_work,
+        moe_grouped_gemm(m, m->dn[0], m->dn_data, m->dn_scales, m->dn_exps, m->hbuf, T * (m->k + m->S), nullptr,
+                         max_work,
                          EpiGemmMoeStore{m->ybuf, (int)m->d});
     }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, s, m->ybuf, m->token_slot,

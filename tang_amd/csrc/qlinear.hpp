@@ -799,11 +799,21 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
 // int4 GEMM on MFMA (v_mfma_f32_16x16x32_f16), for larger m.
 // Workgroup: 4 waves stacked along n, each owning RT 16-row tiles; CB blocks
 // of 16 activation rows.  Per group (K = 32 = one MFMA) a lane dequantises its
-// eight weights to f16 as (n-8)*scale (exact n-8 via the 1024+n magic, one f16
-// rounding of the product) and the activations are rounded to f16.  B tiles
-// (activations for one group-quad, permuted to the nibble-pair order) are
-// staged in LDS.  With KS > 1 each workgroup covers a K slice and writes f32
-// partials [KS][m][n] that q4_splitk_reduce sums in a fixed order.
+// eight weights to f16 as (n-8)*s' (exact n-8 via the 1024+n magic, one f16
+// rounding of the product).  The activations come prepared (f16, permuted,
+// see q4_gemm_xprep_kernel) and go through LDS.  With KS > 1 each workgroup
+// covers a K slice and writes f32 partials [KS][m][n] that
+// splitk_reduce_kernel sums in a fixed order.
+//
+// Range: f16 holds 2^-14..65504 at full precision, far less than the f32 /
+// bf16 inputs of the reference's f64 q4_matvec (quantize.rs:256-289).  Both
+// operands are therefore scaled by powers of two into f16's range and the
+// result scaled back exactly: activation row m is stored as x * 2^-xexp[m]
+// (its largest magnitude in [2^12, 2^13)), weight row n uses
+// s' = s * 2^-wexp[n] (its largest scale in [2^8, 2^9), so |(q-8) s'| <=
+// 2^12), and y[m][n] = ldexp(acc, xexp[m] + wexp[n]).  Values more than 2^26
+// below their row's largest keep less than f16's 11 bits; their share of the
+// sum is below f32 rounding of the large terms.
 // ---------------------------------------------------------------------------
 
 // out[k] = f16 pair (element k, element k+4) of the word, each (n-8)*scale.
@@ -826,6 +836,17 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
+// Exponent that brings a row whose largest magnitude is mx to [2^(top-1),
+// 2^top): mx * 2^-e lands there.  0 for an all-zero or non-finite row.
+__host__ __device__ inline int range_exp(float mx, int top) {
+    if (!(mx > 0.0f) || !(mx <= 3.402823466e38f)) return 0;
+    int E;
+    (void)frexpf(mx, &E);  // mx = f * 2^E, f in [0.5, 1)
+    return E - top;
+}
+constexpr int XPREP_TOP = 13;  // prepared activations: row maximum in [2^12, 2^13)
+constexpr int WSCALE_TOP = 9;  // weight scales: row maximum in [2^8, 2^9)
+
 // Sources of the MFMA GEMM: which weights a workgroup multiplies and which
 // activation rows it takes.  Rows are local to the workgroup's block of
 // CB*16 rows (0 <= m < mrows).
@@ -833,7 +854,8 @@ struct GemmDense {
     static constexpr bool GROUPED = false;
     int M;
     template <typename ST>
-    __device__ __forceinline__ bool select(int by, int rows_per_block, const uint4*& wt, const ST*& sc, int& mrows) {
+    __device__ __forceinline__ bool select(int by, int rows_per_block, const uint4*& wt, const ST*& sc,
+                                           const int*& wexp, int& mrows) {
         m0 = by * rows_per_block;
         mrows = min(rows_per_block, M - m0);
         return true;
@@ -844,8 +866,9 @@ struct GemmDense {
 };
 
 // Epilogue of the MFMA GEMM: D fragment (weight rows n0..n0+3, activation
-// row m) of one lane; `live` is false for rows past the block or the matrix.
-// Called by every lane (pairing epilogues shuffle).
+// row m) of one lane, already scaled back to the true result; `live` is false
+// for rows past the block or the matrix.  Called by every lane (pairing
+// epilogues shuffle).
 struct EpiGemmStore {
     float* y;
     int ldy;
@@ -860,53 +883,84 @@ struct EpiGemmStore {
     }
 };
 
-// Activations for the MFMA GEMM converted once per call (XP mode): f16 with
-// the rounding the GEMM's own staging applies, each 8-value chunk already in
-// nibble-pair order (x0,x4,x1,x5,x2,x6,x3,x7), rows zero-padded to Kp.
+// Activations prepared for the MFMA GEMM: one workgroup per row.  Pass 1
+// finds the row's largest magnitude, pass 2 writes x * 2^-xexp[row] as f16
+// (RNE; exact for a bf16 input within 2^26 of the row maximum), each 8-value
+// chunk in nibble-pair order (x0,x4,x1,x5,x2,x6,x3,x7), zero past K up to Kp.
+// Row r of the output is input row rows[r] (rows == nullptr: row r).
 template <bool XF32>
-__global__ __launch_bounds__(256) void q4_gemm_xprep_kernel(const void* __restrict__ xin, int ldx, int K, int Kp,
-                                                            int M, uint4* __restrict__ out) {
-    const int cpr = Kp >> 3;
-    const size_t total = (size_t)M * cpr;
-    const bool vec = (ldx & 7) == 0 && (((uintptr_t)xin) & 15) == 0;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-        const int m = (int)(i / cpr), k0 = (int)(i % cpr) * 8;
-        float xv[8];
+__device__ __forceinline__ void xprep_load8(const void* xin, size_t ldx, int row, int K, int k0, bool vec, float xv[8]) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) xv[e] = 0.0f;
-        if (XF32) {
-            const float* xr = (const float*)xin + (size_t)m * ldx;
-            if (vec && k0 + 8 <= K) {
-                const float4 a = *(const float4*)(xr + k0), b = *(const float4*)(xr + k0 + 4);
-                xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-                xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
-            } else {
-                for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = xr[k0 + e];
+    for (int e = 0; e < 8; e++) xv[e] = 0.0f;
+    if (XF32) {
+        const float* xr = (const float*)xin + (size_t)row * ldx;
+        if (vec && k0 + 8 <= K) {
+            const float4 a = *(const float4*)(xr + k0), b = *(const float4*)(xr + k0 + 4);
+            xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+            xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        } else {
+            for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = xr[k0 + e];
+        }
+    } else {
+        const uint16_t* xr = (const uint16_t*)xin + (size_t)row * ldx;
+        if (vec && k0 + 8 <= K) {
+            const uint4 a = *(const uint4*)(xr + k0);
+            const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
+                xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
             }
         } else {
-            const uint16_t* xr = (const uint16_t*)xin + (size_t)m * ldx;
-            if (vec && k0 + 8 <= K) {
-                const uint4 a = *(const uint4*)(xr + k0);
-                const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
-                    xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
-                }
-            } else {
-                for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = bf16_bits_to_f32(xr[k0 + e]);
-            }
+            for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = bf16_bits_to_f32(xr[k0 + e]);
         }
-        out[i] = make_uint4(pack_half2(xv[0], xv[4]), pack_half2(xv[1], xv[5]), pack_half2(xv[2], xv[6]),
-                            pack_half2(xv[3], xv[7]));
     }
 }
 
-template <int RT, int CB, bool XF32, typename ST, typename Src = GemmDense, typename Epi = EpiGemmStore,
-          bool XP = false>
+// Largest magnitude over a 256-thread workgroup (every thread gets it).
+__device__ __forceinline__ float block_absmax256(float v, float* red4) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+}
+
+template <bool XF32>
+__global__ __launch_bounds__(256) void q4_gemm_xprep_kernel(const void* __restrict__ xin, int ldx, int K, int Kp,
+                                                            const int* __restrict__ rows, uint4* __restrict__ out,
+                                                            int* __restrict__ xexp) {
+    __shared__ float red4[4];
+    const int r = blockIdx.x;
+    const int row = rows ? rows[r] : r;
+    const int cpr = Kp >> 3;
+    const bool vec = (ldx & 7) == 0 && (((uintptr_t)xin) & 15) == 0;
+    float mx = 0.0f;
+    for (int c = threadIdx.x; c < cpr; c += 256) {
+        float xv[8];
+        xprep_load8<XF32>(xin, (size_t)ldx, row, K, c * 8, vec, xv);
+#pragma unroll
+        for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(xv[e]));
+    }
+    const int e = range_exp(block_absmax256(mx, red4), XPREP_TOP);
+    if (threadIdx.x == 0) xexp[r] = e;
+    for (int c = threadIdx.x; c < cpr; c += 256) {  // second read: L2 hits
+        float xv[8];
+        xprep_load8<XF32>(xin, (size_t)ldx, row, K, c * 8, vec, xv);
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = __builtin_amdgcn_ldexpf(xv[i], -e);
+        out[(size_t)r * cpr + c] = make_uint4(pack_half2(xv[0], xv[4]), pack_half2(xv[1], xv[5]),
+                                              pack_half2(xv[2], xv[6]), pack_half2(xv[3], xv[7]));
+    }
+}
+
+// xin: prepared rows (f16, ldx = Kp halves, row exponents xexp); wexp: the
+// weight rows' scale exponents (th_qweight::row_exp).
+template <int RT, int CB, typename ST, typename Src = GemmDense, typename Epi = EpiGemmStore>
 __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restrict__ wt,
-                                                           const ST* __restrict__ sc,
-                                                           const void* __restrict__ xin, Epi epi, Src src,
+                                                           const ST* __restrict__ sc, const int* __restrict__ wexp,
+                                                           const uint16_t* __restrict__ xin,
+                                                           const int* __restrict__ xexp, Epi epi, Src src,
                                                            int N, int K, int Kp, int ldx, int gq_per_split) {
     // LDS B tile: [CB][4 j][4 q][16 col] uint4 (8 f16 each)
     // two B tiles: the next group-quad's is written while this one is read,
@@ -916,9 +970,11 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     {
         const uint4* wsel = wt;
         const ST* ssel = sc;
-        if (!src.select((int)blockIdx.y, CB * 16, wsel, ssel, mrows)) return;
+        const int* esel = wexp;
+        if (!src.select((int)blockIdx.y, CB * 16, wsel, ssel, esel, mrows)) return;
         wt = wsel;
         sc = ssel;
+        wexp = esel;
     }
     const int GQ = Kp >> 7;
     // a scalar wave index pays off for the grouped (MoE) source and costs
@@ -931,14 +987,17 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     const int gq0 = blockIdx.z * gq_per_split;
     const int gq1 = min(GQ, gq0 + gq_per_split);
 
-    const bool vec = (ldx & 7) == 0 && (((uintptr_t)xin) & 15) == 0;
     float4_t acc[RT][CB];
 #pragma unroll
     for (int a = 0; a < RT; a++)
 #pragma unroll
         for (int b = 0; b < CB; b++) acc[a][b] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    // scale exponent of this lane's weight row (row r of each tile)
+    int wneg[RT];
+#pragma unroll
+    for (int a = 0; a < RT; a++) wneg[a] = -wexp[min(tile0 + a, NT - 1) * 16 + r];
 
-    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xin, 0x7FFFFFF0u);  // prepared rows (XP), in-range offsets only
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xin, 0x7FFFFFF0u);  // in-range offsets only
     // staging assignment: CB*16 cols * 16 chunks (4 groups x 4 quads) = CB*256 chunks
     auto load_x = [&](int gq, uint4 (&regs)[CB]) {
 #pragma unroll
@@ -950,53 +1009,15 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
             const int cb = idx >> 8;
             const int ml = cb * 16 + col;
             const int k0 = gq * 128 + j * 32 + qq * 8;
-            if constexpr (XP) {  // prepared: f16, permuted, padded (ldx = Kp)
-                if constexpr (Src::GROUPED) {  // short work items: skip the loads of empty rows
-                    regs[i] = ml < mrows ? *(const uint4*)((const uint16_t*)xin + (size_t)src.x_row(ml) * ldx + k0)
-                                         : make_uint4(0, 0, 0, 0);
-                } else {
-                    // branch-free: rows past mrows re-read the last live row
-                    // (a finite copy whose D columns are never stored)
-                    const uint32_t off = (uint32_t)(src.x_row(min(ml, mrows - 1)) * ldx + k0) * 2u;
-                    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
-                    regs[i] = make_uint4(v.x, v.y, v.z, v.w);
-                }
+            if constexpr (Src::GROUPED) {  // short work items: skip the loads of empty rows
+                regs[i] = ml < mrows ? *(const uint4*)(xin + (size_t)src.x_row(ml) * ldx + k0)
+                                     : make_uint4(0, 0, 0, 0);
             } else {
-            float xv[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) xv[e] = 0.0f;
-            if (ml < mrows) {
-                const int m = src.x_row(ml);
-                if (XF32) {
-                    const float* xr = (const float*)xin + (size_t)m * ldx;
-                    if (vec && k0 + 8 <= K) {
-                        float4 a = *(const float4*)(xr + k0), b = *(const float4*)(xr + k0 + 4);
-                        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-                        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
-                    } else {
-                        for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = xr[k0 + e];
-                    }
-                } else {
-                    const uint16_t* xr = (const uint16_t*)xin + (size_t)m * ldx;
-                    if (vec && k0 + 8 <= K) {
-                        uint4 a = *(const uint4*)(xr + k0);
-                        uint32_t w4[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            xv[2 * e] = bf16_bits_to_f32(w4[e] & 0xFFFF);
-                            xv[2 * e + 1] = bf16_bits_to_f32(w4[e] >> 16);
-                        }
-                    } else {
-                        for (int e = 0; e < 8; e++) if (k0 + e < K) xv[e] = bf16_bits_to_f32(xr[k0 + e]);
-                    }
-                }
-            }
-            uint4 o;
-            o.x = pack_half2(xv[0], xv[4]);
-            o.y = pack_half2(xv[1], xv[5]);
-            o.z = pack_half2(xv[2], xv[6]);
-            o.w = pack_half2(xv[3], xv[7]);
-            regs[i] = o;
+                // branch-free: rows past mrows re-read the last live row
+                // (a finite copy whose D columns are never stored)
+                const uint32_t off = (uint32_t)(src.x_row(min(ml, mrows - 1)) * ldx + k0) * 2u;
+                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+                regs[i] = make_uint4(v.x, v.y, v.z, v.w);
             }
         }
     };
@@ -1042,7 +1063,7 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
 #pragma unroll
             for (int a = 0; a < RT; a++) {
                 const uint32_t w = j == 0 ? wcur[a].x : j == 1 ? wcur[a].y : j == 2 ? wcur[a].z : wcur[a].w;
-                const _Float16 s = (_Float16)scur.get(a, j);
+                const _Float16 s = (_Float16)__builtin_amdgcn_ldexpf(scur.get(a, j), wneg[a]);
                 const half2_t s2 = {s, s};
                 half2_t p[4];
                 nib_pairs_f16(w, s2, p);
@@ -1062,14 +1083,25 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     }
 
     // D layout: lane holds rows 4*(lane/16)+i (weight rows) of column lane%16.
+    int xe[CB];
+#pragma unroll
+    for (int b = 0; b < CB; b++) {
+        const int ml = b * 16 + r;
+        xe[b] = xexp[src.x_row(ml < mrows ? ml : 0)];
+    }
 #pragma unroll
     for (int a = 0; a < RT; a++) {
         const int n0 = (tile0 + a) * 16 + 4 * q;
+        const int4 we = *(const int4*)(wexp + min(tile0 + a, NT - 1) * 16 + 4 * q);
+        const int wev[4] = {we.x, we.y, we.z, we.w};
 #pragma unroll
         for (int b = 0; b < CB; b++) {
             const int ml = b * 16 + r;
             const bool live = ml < mrows && tile0 + a < NT;
-            epi(src.out_row(live ? ml : 0), n0, N, live, acc[a][b]);
+            float4_t v;
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = __builtin_amdgcn_ldexpf(acc[a][b][i], xe[b] + wev[i]);
+            epi(src.out_row(live ? ml : 0), n0, N, live, v);
         }
     }
 }

@@ -19,10 +19,12 @@ from llama_ref import CONFIG_7B, OracleLlama  # noqa: E402
 # top-2 logit gap comparable to the f32-vs-f64 rounding of two correct
 # implementations; with first token 1 the gap at step 59 is 1.3e-5 and the
 # token there depends on summation order).  Token 10 was chosen by scanning
-# first tokens 1..40 on the device for the largest minimum top-2 gap among
-# trajectories that visit more than one token (min gap 9.1e-5, 3 distinct
-# tokens); the gaps of every step are stored with the tokens, and so are the
-# five largest logits of every step, for the teacher-forced check.
+# first tokens 1..40 on the device for trajectories that visit more than one
+# token; its smallest top-2 gap in the oracle's run is 3.4e-5 (step 59) and it
+# visits 3 distinct tokens.  The gaps of every step are stored with the
+# tokens, and so are the five largest logits of every step, for the
+# teacher-forced check.  The varied-input check is the teacher-forced golden
+# of make_decode_golden_forced.py (128 distinct input tokens).
 SEED, KV_SEED, PREFILL, FIRST_TOKEN, STEPS = 3, 33, 2048, 10, 128
 
 

@@ -99,9 +99,8 @@ def _golden():
 
 @pytest.mark.skipif(not os.path.exists(GOLDEN), reason="golden vectors not generated")
 def test_7b_decode_free_running_matches_golden(dev):
-    """128 greedy steps from position 2048: identical tokens up to the first
-    step the oracle itself cannot decide (and there a token tied with the
-    oracle's maximum); the final logits within 1e-3."""
+    """128 greedy steps from position 2048: all 128 tokens identical to the
+    oracle's, and the final logits within the bf16-activation bar."""
     g = _golden()
     cfg = CONFIG_7B
     m = device_llama(dev, cfg, g["seed"], g["kv_seed"], g["prefill"])
@@ -109,23 +108,15 @@ def test_7b_decode_free_running_matches_golden(dev):
         toks, logits = device_generate(m, cfg, g["first_token"], g["prefill"], g["steps"])
     finally:
         capi.lib().th_llama_destroy(m)
-    undecided = [i for i in range(g["steps"]) if g["margins"][i] <= DECIDED * g["logit_absmax"][i]]
-    stop = undecided[0] if undecided else g["steps"]
-    print("first undecided step:", stop, "min margin %.3e" % min(g["margins"]))
     mism = [i for i, (a, b) in enumerate(zip(toks, g["tokens"])) if a != b]
-    print("first mismatches:", mism[:5])
-    assert list(toks[:stop]) == g["tokens"][:stop]
-    if stop < g["steps"]:
-        ids, vals = g["top5_ids"][stop], g["top5_logits"][stop]
-        tied = [j for j, v in zip(ids, vals) if v >= vals[0] - DECIDED * g["logit_absmax"][stop]]
-        assert int(toks[stop]) in tied
-    if not mism:
-        # after 128 autoregressive steps the device's own KV rows feed every
-        # step: differences compound, so the bar is the bf16-activation one
-        # (linear inputs are bf16 as in cuda.rs:22); single steps are held to
-        # 1e-3 by the teacher-forced test
-        last = np.array(g["last_logits_head"], np.float32)
-        assert max_abs_rel(logits[: last.size], last) < 2e-2
+    print("min margin %.3e; mismatching steps %s" % (min(g["margins"]), mism[:8]))
+    assert list(toks) == g["tokens"]
+    # after 128 autoregressive steps the device's own KV rows feed every step:
+    # differences compound, so the bar is the bf16-activation one (linear
+    # inputs are bf16 as in cuda.rs:22); single steps are held to LOGIT_TOL
+    # by the teacher-forced tests
+    last = np.array(g["last_logits_head"], np.float32)
+    assert max_abs_rel(logits[: last.size], last) < 2e-2
 
 
 @pytest.mark.skipif(not os.path.exists(GOLDEN), reason="golden vectors not generated")
@@ -152,6 +143,40 @@ def test_7b_decode_teacher_forced_128_steps(dev):
     finally:
         capi.lib().th_llama_destroy(m)
     print("steps with the oracle's exact token: %d / %d" % (exact, g["steps"]))
+
+
+FORCED = os.path.join(os.path.dirname(__file__), "golden", "llama7b_forced.json")
+
+
+@pytest.mark.skipif(not os.path.exists(FORCED), reason="golden vectors not generated")
+def test_7b_decode_teacher_forced_distinct_tokens(dev):
+    """128 steps on 128 distinct seeded input tokens (each step reads a
+    different embedding row and appends its own K/V rows): the first 256
+    logits and the oracle's five largest agree to LOGIT_TOL of the step's
+    largest |logit|, and the token equals the oracle's wherever the oracle's
+    top-2 gap decides it (otherwise it is one tied within the bar)."""
+    g = json.load(open(FORCED))
+    cfg = CONFIG_7B
+    m = device_llama(dev, cfg, g["seed"], g["kv_seed"], g["prefill"])
+    exact = decided = 0
+    try:
+        for i, tok_in in enumerate(g["tokens_in"]):
+            toks, logits = device_generate(m, cfg, tok_in, g["prefill"] + i, 1)
+            amax = g["logit_absmax"][i]
+            tol = LOGIT_TOL * amax
+            head = np.array(g["logits_head"][i], np.float32)
+            assert np.max(np.abs(logits[: head.size] - head)) <= tol, i
+            ids, vals = g["top5_ids"][i], g["top5_logits"][i]
+            assert np.max(np.abs(logits[ids] - np.array(vals, np.float32))) <= tol, i
+            if g["margins"][i] > DECIDED * amax:
+                decided += 1
+                assert int(toks[0]) == g["tokens"][i], (i, int(toks[0]), g["tokens"][i])
+            else:
+                assert int(toks[0]) in [j for j, v in zip(ids, vals) if v >= vals[0] - tol], i
+            exact += int(toks[0]) == g["tokens"][i]
+    finally:
+        capi.lib().th_llama_destroy(m)
+    print("exact tokens %d / %d (%d decided by the oracle)" % (exact, len(g["tokens_in"]), decided))
 
 
 def _device_steps_oracle_sampler(dev, cfg, prompt, prefill, steps, seed, stop=None, **kw):
@@ -281,6 +306,11 @@ def test_llama_from_safetensors_matches_oracle(dev, tmp_path, tied):
         stored["model.layers.%d.post_attention_layernorm.weight" % l] = rng.normal(1, 0.1, d).astype(np.float32)
     stored["model.layers.0.self_attn.q_proj.weight"] = stored["model.layers.0.self_attn.q_proj.weight"].astype(
         np.float16)
+    # near-zero rows and a zero row: block scales below f16's normal range
+    # (stored as f16 subnormals or zero) must load, not abort
+    stored["model.layers.1.mlp.down_proj.weight"][:3] *= np.float32(1e-6)
+    stored["model.layers.1.mlp.down_proj.weight"][3] = 0.0
+    stored["model.layers.1.self_attn.v_proj.weight"][5, :64] *= np.float32(1e-4)
     path = tmp_path / "model.safetensors"
     save_file(stored, str(path))
     tensors = {k: v.astype(np.float32) for k, v in stored.items()}
