@@ -87,6 +87,10 @@ int th_buffer_zero(th_buffer* buf);
  * (ComputeDevice::copy_buffer-style helper; also the known-size copy the
  * HBM-traffic counters are calibrated against). */
 int th_buffer_copy(th_buffer* dst, const th_buffer* src);
+/* Copy n elements src[src_offset..] -> dst[dst_offset..] (same dtype) on the
+ * device stream: slice_buffer / write_into (device.rs:839-850) and the column
+ * moves of extract_columns / concat_columns without a host round trip. */
+int th_buffer_copy_region(th_buffer* dst, size_t dst_offset, const th_buffer* src, size_t src_offset, size_t n);
 /* Element-wise dtype conversion between f32, bf16 and f16 buffers of equal
  * length; f32->bf16 rounds as crates/tang-compute/src/cuda.rs:22-27,
  * f32->f16 is IEEE round-to-nearest-even (kernels BF16_TO_F32_CUDA /
@@ -165,6 +169,48 @@ int th_gemv_q8(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w
  * earlier, for any iters. */
 int th_bench_linear(th_device* dev, const th_buffer* x, size_t m, th_qweight* const* ws, size_t n_w,
                     th_buffer* y, size_t iters, int use_graph, float* ms);
+
+/* ---- dense operators (ComputeDevice methods for unquantized weights) ------
+ * f32 buffers unless stated; all calls enqueue on the device stream. */
+
+/* C[m][n] (+)= op(A) . op(B): ComputeDevice::matmul (device.rs:103),
+ * matmul_accumulate (:391), matmul_b_transposed (:407), matmul_a_transposed
+ * (:422) and matmul_accumulate_a_transposed (:437) in one call.  A is [m][k]
+ * (trans_a: stored [k][m]), B is [k][n] (trans_b: stored [n][k], the
+ * Linear::forward_2d weight layout, modules.rs:56); A and B f32 or bf16, C
+ * f32; accumulate != 0 adds to C.  f32 products, f32 accumulation on MFMA. */
+int th_matmul_ex(th_device* dev, const th_buffer* a, const th_buffer* b, size_t m, size_t k, size_t n, int trans_a,
+                 int trans_b, int accumulate, th_buffer* c);
+/* ComputeDevice::matmul (device.rs:103; CpuDevice cpu.rs:99,760). */
+int th_matmul(th_device* dev, const th_buffer* a, const th_buffer* b, size_t m, size_t k, size_t n, th_buffer* c);
+/* ComputeDevice::matmul_b_transposed (device.rs:407). */
+int th_matmul_b_transposed(th_device* dev, const th_buffer* a, const th_buffer* b, size_t m, size_t k, size_t n,
+                           th_buffer* c);
+/* ComputeDevice::transpose_2d (device.rs:183; cpu.rs:317). */
+int th_transpose_2d(th_device* dev, const th_buffer* in, size_t rows, size_t cols, th_buffer* out);
+/* ComputeDevice::reduce_sum (device.rs:140; cpu.rs:169) over axis of a
+ * row-major tensor of ndim dims; accumulate != 0 is reduce_sum_accumulate
+ * (device.rs:451).  Sums in the reference's order: bit-identical. */
+int th_reduce_sum(th_device* dev, const th_buffer* in, const size_t* shape, size_t ndim, size_t axis, int accumulate,
+                  th_buffer* out);
+/* ComputeDevice::bias_add (device.rs:378): out[i] = matrix[i] + bias[i % dim]. */
+int th_bias_add(th_device* dev, const th_buffer* matrix, const th_buffer* bias, size_t numel, size_t dim,
+                th_buffer* out);
+/* ComputeDevice::add_assign (device.rs:767; cpu.rs:650): dst += src, equal lengths. */
+int th_add_assign(th_device* dev, th_buffer* dst, const th_buffer* src);
+
+/* Run-time compiled element-wise kernels: the source tang-expr generates for
+ * ComputeDevice::elementwise (device.rs:93; the CUDA backend's path is
+ * cuda.rs:1135-1190), i.e. a kernel
+ *   extern "C" __global__ void <entry>(const float* in0, ..., float* outputs,
+ *                                      const unsigned int count)
+ * with one thread per element, compiled for gfx950 with hiprtc and loaded as a
+ * hipModule.  th_elementwise launches it over numel elements (256-thread
+ * workgroups) with the n_inputs f32 input buffers and the f32 output. */
+typedef struct th_kernel th_kernel;
+int th_kernel_compile(th_device* dev, const char* source, const char* entry, th_kernel** out);
+int th_kernel_free(th_kernel* k);
+int th_elementwise(th_kernel* k, const th_buffer* const* inputs, size_t n_inputs, size_t numel, th_buffer* out);
 
 /* ---- decode ops (f32 buffers unless stated) ---------------------------- */
 

@@ -62,6 +62,10 @@ _SIG = {
     "or_add": ([_P, _P, _S, _P], None),
     "or_embedding": ([_P, _P, _S, _S, _P], None),
     "or_softmax": ([_P, _S, _S, _P], None),
+    "or_matmul": ([_P, _P, _S, _S, _S, _P], None),
+    "or_transpose_2d": ([_P, _S, _S, _P], None),
+    "or_reduce_sum": ([_P, _P, _S, _S, _P], None),
+    "or_bias_add": ([_P, _P, _S, _S, _P], None),
     "or_argmax_f32": ([_P, _S], _S),
     "or_llama_decode_step": ([_P, _P, _P, _P, _I, _I, _P, _I], _I),
     "or_moe_forward": ([_P, _S, _S, _S, _S, _S, _S, _P, _P, _P, _P, _P, _P, _I], None),
@@ -299,3 +303,36 @@ class OracleSampler:
         pa = np.ascontiguousarray(past, np.int32)
         return int(lib().or_sample(ctypes.byref(self.cfg), ctypes.byref(self.state), p(lg), lg.size,
                                    p(pa) if pa.size else None, pa.size))
+
+
+def matmul(a, b, m, k, n):
+    """naive_matmul (cpu.rs:760): f32 sums in k order."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty(m * n, np.float32)
+    lib().or_matmul(p(a), p(b), m, k, n, p(out))
+    return out.reshape(m, n)
+
+
+def transpose_2d(x, rows, cols):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(rows * cols, np.float32)
+    lib().or_transpose_2d(p(x), rows, cols, p(out))
+    return out
+
+
+def reduce_sum(x, shape, axis):
+    x = np.ascontiguousarray(x, np.float32)
+    sh = np.ascontiguousarray(shape, np.uint64)
+    n_out = int(np.prod([d for i, d in enumerate(shape) if i != axis], dtype=np.int64))
+    out = np.empty(n_out, np.float32)
+    lib().or_reduce_sum(p(x), p(sh), len(shape), axis, p(out))
+    return out
+
+
+def bias_add(m, bias, numel, dim):
+    m = np.ascontiguousarray(m, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    out = np.empty(numel, np.float32)
+    lib().or_bias_add(p(m), p(bias), numel, dim, p(out))
+    return out

@@ -442,6 +442,42 @@ void or_softmax(const float* x, size_t rows, size_t len, float* out) {
     }
 }
 
+/* crates/tang-compute/src/cpu.rs:760-770 naive_matmul (the non-macOS
+ * matmul_impl): C[m][n] = sum_p A[m][p] * B[p][n], one f32 sum per output in
+ * p order. */
+void or_matmul(const float* a, const float* b, size_t m, size_t k, size_t n, float* c) {
+    for (size_t i = 0; i < m; i++)
+        for (size_t j = 0; j < n; j++) {
+            float sum = 0.0f;
+            for (size_t p = 0; p < k; p++) sum += a[i * k + p] * b[p * n + j];
+            c[i * n + j] = sum;
+        }
+}
+
+/* crates/tang-compute/src/cpu.rs:317-326 transpose_2d: out[c][r] = in[r][c]. */
+void or_transpose_2d(const float* in, size_t rows, size_t cols, float* out) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) out[c * rows + r] = in[r * cols + c];
+}
+
+/* crates/tang-compute/src/cpu.rs:169-199 reduce_sum over `axis` of a
+ * row-major tensor: outputs start at 0 and add in (o, a, i) loop order. */
+void or_reduce_sum(const float* in, const size_t* shape, size_t ndim, size_t axis, float* out) {
+    size_t outer = 1, inner = 1;
+    for (size_t d = 0; d < axis; d++) outer *= shape[d];
+    for (size_t d = axis + 1; d < ndim; d++) inner *= shape[d];
+    size_t len = shape[axis];
+    for (size_t i = 0; i < outer * inner; i++) out[i] = 0.0f;
+    for (size_t o = 0; o < outer; o++)
+        for (size_t a = 0; a < len; a++)
+            for (size_t i = 0; i < inner; i++) out[o * inner + i] += in[(o * len + a) * inner + i];
+}
+
+/* crates/tang-compute/src/device.rs:378-386 bias_add: out[i] = m[i] + bias[i % dim]. */
+void or_bias_add(const float* m, const float* bias, size_t numel, size_t dim, float* out) {
+    for (size_t i = 0; i < numel; i++) out[i] = m[i] + bias[i % dim];
+}
+
 /* crates/tang-infer/src/sampling.rs:184-194 argmax: first strictly greater
  * value wins (ties resolve to the lowest index). */
 size_t or_argmax_f32(const float* v, size_t n) {

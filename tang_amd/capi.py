@@ -59,6 +59,7 @@ SIGNATURES = {
     "th_buffer_info": ([_P, _P, _P], _I),
     "th_buffer_zero": ([_P], _I),
     "th_buffer_copy": ([_P, _P], _I),
+    "th_buffer_copy_region": ([_P, _S, _P, _S, _S], _I),
     "th_convert": ([_P, _P, _P], _I),
     "th_q4_upload_blocks": ([_P, _P, _S, _S, _I, _P], _I),
     "th_q4_upload_packed": ([_P, _P, _P, _I, _S, _S, _P], _I),
@@ -110,6 +111,16 @@ SIGNATURES = {
     "th_st_upload_q4": ([_P, _P, ctypes.c_char_p, _P], _I),
     "th_st_upload_q8": ([_P, _P, ctypes.c_char_p, _P], _I),
     "th_mla_decode": ([_P, _P, _P, _P, _S, _S, _S, _S, _S, _S, _S, _P, _P, _F, _P], _I),
+    "th_matmul_ex": ([_P, _P, _P, _S, _S, _S, _I, _I, _I, _P], _I),
+    "th_matmul": ([_P, _P, _P, _S, _S, _S, _P], _I),
+    "th_matmul_b_transposed": ([_P, _P, _P, _S, _S, _S, _P], _I),
+    "th_transpose_2d": ([_P, _P, _S, _S, _P], _I),
+    "th_reduce_sum": ([_P, _P, _P, _S, _S, _I, _P], _I),
+    "th_bias_add": ([_P, _P, _P, _S, _S, _P], _I),
+    "th_add_assign": ([_P, _P, _P], _I),
+    "th_kernel_compile": ([_P, ctypes.c_char_p, ctypes.c_char_p, _P], _I),
+    "th_kernel_free": ([_P], _I),
+    "th_elementwise": ([_P, _P, _S, _S, _P], _I),
     "th_synth_seed": ([_U64, _U64, _U64], _U64),
     "th_synth_q4": ([_U64, _S, _S, _F, _F, _P, _P], _I),
     "th_synth_q8_rowwise": ([_U64, _S, _S, _F, _F, _P, _P], _I),
@@ -506,6 +517,51 @@ class HipComputeDevice:
         out = out or self.alloc(B * H * dv)
         check(lib().th_mla_decode(self.handle, q_nope.handle, q_rope.handle, cache.handle, B, H, L, dn, dr, r, dv,
                                   w_uk.handle, w_uv.handle, sm_scale, out.handle))
+        return out
+
+    # ---- dense operators (device.rs matmul / transpose_2d / reduce_sum / ...)
+    def matmul(self, a, b, m, k, n, trans_a=False, trans_b=False, accumulate_into=None):
+        c = accumulate_into if accumulate_into is not None else self.alloc(m * n)
+        check(lib().th_matmul_ex(self.handle, a.handle, b.handle, m, k, n, int(trans_a), int(trans_b),
+                                 int(accumulate_into is not None), c.handle))
+        return c
+
+    def matmul_b_transposed(self, a, b, m, k, n):
+        return self.matmul(a, b, m, k, n, trans_b=True)
+
+    def transpose_2d(self, buf, rows, cols):
+        out = self.alloc(rows * cols)
+        check(lib().th_transpose_2d(self.handle, buf.handle, rows, cols, out.handle))
+        return out
+
+    def reduce_sum(self, buf, shape, axis, accumulate_into=None):
+        n_out = 1
+        for i, d in enumerate(shape):
+            if i != axis:
+                n_out *= d
+        out = accumulate_into if accumulate_into is not None else self.alloc(n_out)
+        sh = (ctypes.c_size_t * len(shape))(*shape)
+        check(lib().th_reduce_sum(self.handle, buf.handle, sh, len(shape), axis, int(accumulate_into is not None),
+                                  out.handle))
+        return out
+
+    def bias_add(self, matrix, bias, numel, dim):
+        out = self.alloc(numel)
+        check(lib().th_bias_add(self.handle, matrix.handle, bias.handle, numel, dim, out.handle))
+        return out
+
+    def add_assign(self, dst, src):
+        check(lib().th_add_assign(self.handle, dst.handle, src.handle))
+
+    def compile_kernel(self, source, entry="k0"):
+        h = ctypes.c_void_p()
+        check(lib().th_kernel_compile(self.handle, source.encode(), entry.encode(), ctypes.byref(h)))
+        return h
+
+    def elementwise(self, kernel, inputs, numel):
+        out = self.alloc(numel)
+        arr = (ctypes.c_void_p * max(len(inputs), 1))(*[b.handle for b in inputs])
+        check(lib().th_elementwise(kernel, arr, len(inputs), numel, out.handle))
         return out
 
     def close(self):

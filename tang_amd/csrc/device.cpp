@@ -366,6 +366,19 @@ int th_buffer_copy(th_buffer* dst, const th_buffer* src) {
     TH_API_END
 }
 
+int th_buffer_copy_region(th_buffer* dst, size_t dst_offset, const th_buffer* src, size_t src_offset, size_t n) {
+    TH_API_BEGIN
+    TH_REQUIRE(dst && src && dst->dev == src->dev, "buffers must share a device");
+    TH_REQUIRE(dst->dtype == src->dtype, "buffers must share a dtype");
+    TH_REQUIRE(src_offset <= src->n && n <= src->n - src_offset, "source range out of bounds");
+    TH_REQUIRE(dst_offset <= dst->n && n <= dst->n - dst_offset, "destination range out of bounds");
+    const size_t es = dtype_size(dst->dtype);
+    if (n)
+        TH_HIP(hipMemcpyAsync((char*)dst->ptr + dst_offset * es, (const char*)src->ptr + src_offset * es, n * es,
+                              hipMemcpyDeviceToDevice, dst->dev->stream));
+    TH_API_END
+}
+
 int th_buffer_info(const th_buffer* b, th_dtype* dt, size_t* n) {
     TH_API_BEGIN
     TH_REQUIRE(b, "null buffer");

@@ -248,7 +248,8 @@ int th_add(th_device* dev, const th_buffer* a, const th_buffer* b, size_t n, th_
 int th_embedding(th_device* dev, const th_buffer* w, const th_buffer* ids, size_t seq_len, size_t dim, th_buffer* out) {
     TH_API_BEGIN
     TH_REQUIRE(dev && w && ids && out, "null argument");
-    TH_REQUIRE(ids->dtype == TH_U32 || ids->dtype == TH_I32, "ids must be u32");
+    // u32 ids, or an f32 buffer holding their bit patterns (cpu.rs:160, to_bits)
+    TH_REQUIRE(ids->dtype == TH_U32 || ids->dtype == TH_I32 || ids->dtype == TH_F32, "ids must be u32");
     require_len_any(ids, seq_len, "ids");
     require_len(out, TH_F32, seq_len * dim, "out");
     TH_REQUIRE(dim > 0 && w->n % dim == 0, "weight length must be a multiple of dim");

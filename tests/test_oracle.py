@@ -393,3 +393,67 @@ def test_mla_oracle_matches_explicit_decompression():
             pr /= pr.sum()
             ref[b, h] = pr @ v
     assert max_abs_rel(out, ref.reshape(-1)) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Dense operators: matmul, transpose_2d, reduce_sum, bias_add
+# (crates/tang-compute/src/cpu.rs:169-199,317-326,760-770; device.rs:378)
+# ---------------------------------------------------------------------------
+
+def test_matmul_kats():  # cpu.rs:785-822
+    assert oracle.matmul([1, 0, 0, 1], [1, 2, 3, 4], 2, 2, 2).reshape(-1).tolist() == [1, 2, 3, 4]
+    assert oracle.matmul([1, 2], [3, 4], 1, 2, 1)[0, 0] == 11.0
+    c = oracle.matmul([1, 2, 3, 4, 5, 6], [7, 8, 9, 10, 11, 12], 2, 3, 2)
+    assert c.reshape(-1).tolist() == [58.0, 64.0, 139.0, 154.0]
+
+
+def test_matmul_sequential_order_and_numpy():
+    """Bit-equal to a sequential f32 loop on a small case (the reference's
+    order), and within f32 rounding of numpy float64 on a larger one."""
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal((3, 7)).astype(np.float32)
+    b = rng.standard_normal((7, 5)).astype(np.float32)
+    want = np.zeros((3, 5), np.float32)
+    for i in range(3):
+        for j in range(5):
+            s = np.float32(0)
+            for p in range(7):
+                s = np.float32(s + np.float32(a[i, p] * b[p, j]))
+            want[i, j] = s
+    assert np.array_equal(oracle.matmul(a, b, 3, 7, 5), want)
+    a = rng.standard_normal((40, 300)).astype(np.float32)
+    b = rng.standard_normal((300, 33)).astype(np.float32)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert max_abs_rel(oracle.matmul(a, b, 40, 300, 33), ref) < 1e-5
+    # a transposed operand would fail this: A is 40x300, A^T B is not defined
+    assert not np.allclose(oracle.matmul(a[:33, :33].copy(), b[:33].copy(), 33, 33, 33),
+                           (a[:33, :33].T.astype(np.float64) @ b[:33].astype(np.float64)), rtol=1e-3)
+
+
+def test_transpose_kat_and_numpy():  # cpu.rs:986-994
+    assert oracle.transpose_2d([1, 2, 3, 4, 5, 6], 2, 3).tolist() == [1, 4, 2, 5, 3, 6]
+    x = np.random.default_rng(1).standard_normal((13, 70)).astype(np.float32)
+    assert np.array_equal(oracle.transpose_2d(x, 13, 70), x.T.reshape(-1))
+
+
+def test_reduce_sum_kats_and_loops():  # cpu.rs:869-890
+    d = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    assert oracle.reduce_sum(d, [2, 3], 1).tolist() == [6.0, 15.0]
+    assert oracle.reduce_sum(d, [2, 3], 0).tolist() == [5.0, 7.0, 9.0]
+    rng = np.random.default_rng(2)
+    shape = [3, 5, 4]
+    x = rng.standard_normal(shape).astype(np.float32)
+    for axis in range(3):
+        got = oracle.reduce_sum(x.reshape(-1), shape, axis)
+        want = np.zeros([s for i, s in enumerate(shape) if i != axis], np.float32)
+        moved = np.moveaxis(x, axis, 0)
+        for a in range(shape[axis]):  # sequential f32 adds in axis order
+            want = (want + moved[a]).astype(np.float32)
+        assert np.array_equal(got, want.reshape(-1)), axis
+
+
+def test_bias_add_vs_numpy():
+    rng = np.random.default_rng(3)
+    m = rng.standard_normal(6 * 7).astype(np.float32)
+    b = rng.standard_normal(7).astype(np.float32)
+    assert np.array_equal(oracle.bias_add(m, b, 42, 7), (m.reshape(6, 7) + b).reshape(-1))
