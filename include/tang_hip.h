@@ -158,6 +158,19 @@ int th_st_upload_q8(th_device* dev, const th_st_file* f, const char* name, th_qw
 int th_gemm_q4(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y);
 int th_gemv_q8(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y);
 
+/* Allocation-free form of th_gemm_q4 (no counterpart in the reference): for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results as th_gemm_q4, but the MFMA path's workspace (the
+ * prepared activations, then the split-K partials) is a fixed per-GPU device
+ * array of TH_NOALLOC_SCRATCH_BYTES, not an allocation: the call makes no
+ * hipMalloc / hipFree.  Fails with TH_ERR_INVALID when the prepared
+ * activations, about 2*m*K bytes, do not fit (split-K is narrowed to what
+ * fits).  Every call on one GPU shares the array: calls that overlap on one
+ * GPU (two streams, two threads) race. */
+#define TH_NOALLOC_SCRATCH_BYTES (64u << 20)
+int th_gemm_q4_noalloc(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y);
+
 /* Benchmark helper (no reference counterpart): enqueue `iters` calls of
  * th_gemm_q4 / th_gemv_q8 (by the weights' bit width) on x -> y, cycling
  * through the n_w weights (all of one shape) so the streamed bytes exceed the

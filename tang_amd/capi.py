@@ -70,6 +70,7 @@ SIGNATURES = {
     "th_qweight_free": ([_P], _I),
     "th_gemm_q4": ([_P, _P, _S, _P, _P], _I),
     "th_gemv_q8": ([_P, _P, _S, _P, _P], _I),
+    "th_gemm_q4_noalloc": ([_P, _P, _S, _P, _P], _I),
     "th_bench_linear": ([_P, _P, _S, _P, _S, _P, _S, _I, _P], _I),
     "th_rms_norm": ([_P, _P, _P, _S, _S, _F, _P], _I),
     "th_rms_norm_residual": ([_P, _P, _P, _P, _S, _S, _F, _P, _P], _I),

@@ -67,14 +67,18 @@ struct PreparedX {
 };
 // prepare_x writes that layout for m rows of x (input row rows[r] for output
 // row r when rows is set) into the device's operand workspace.
+// workspace (optional): prepared_x_bytes(m, Kp) bytes to use instead.
 PreparedX prepare_x(th_device* dev, const void* x, bool xf32, size_t m, size_t ldx, size_t K, size_t Kp,
-                    hipStream_t s, const int* rows = nullptr);
+                    hipStream_t s, const int* rows = nullptr, void* workspace = nullptr);
+size_t prepared_x_bytes(size_t m, size_t Kp);
 // The MFMA GEMM on prepared activations, for producers that write the layout
 // directly.  accumulate: y += x.W^T (a fused residual add) instead of y = x.W^T.
 void launch_q4_linear_prepared(const th_qweight* w, PreparedX xp, size_t m, float* y, size_t ldy, hipStream_t s,
                                th_device* dev, bool accumulate = false);
+// ws / ws_bytes (optional): a workspace for the MFMA path (prepared
+// activations, then split-K partials) instead of the device's grow-only one.
 void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
-                      size_t ldy, hipStream_t stream, th_device* dev);
+                      size_t ldy, hipStream_t stream, th_device* dev, void* ws = nullptr, size_t ws_bytes = 0);
 void launch_q8_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
                       size_t ldy, hipStream_t stream);
 

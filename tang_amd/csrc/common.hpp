@@ -82,6 +82,7 @@ struct th_device {
     void* scratch_x = nullptr;  // stream-ordered workspace for GEMM operands prepared in f16
     size_t scratch_x_bytes = 0;
     int* counters = nullptr;  // see device_counters
+    void* noalloc_scratch = nullptr;  // this device's address of the th_gemm_q4_noalloc workspace
     size_t n_counters = 0;
     int live = 0;          // buffers, weights and engines that hold this device
     bool closed = false;   // th_device_destroy ran; the struct waits for live == 0

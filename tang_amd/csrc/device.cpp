@@ -14,6 +14,14 @@
 
 namespace th {
 
+// Workspace of th_gemm_q4_noalloc (the allocation-free GEMM): a file-scope
+// device array, TH_NOALLOC_SCRATCH_BYTES per GPU, held by every GPU the
+// library runs on until the process ends.  Host code never uses its name as
+// an address: th_device_create looks up the array's address on its device
+// (th_device::noalloc_scratch) and kernels receive that.  Every call on one
+// GPU shares it.
+static __device__ __align__(256) unsigned char scratch[TH_NOALLOC_SCRATCH_BYTES];
+
 static thread_local std::string g_last_error;
 void set_last_error(const std::string& msg) { g_last_error = msg; }
 
@@ -237,8 +245,12 @@ int th_device_create(int ordinal, th_device** out) {
     TH_HIP(hipGetDeviceCount(&c));
     TH_REQUIRE(ordinal >= 0 && ordinal < c, "device ordinal out of range");
     TH_HIP(hipSetDevice(ordinal));
+    // this GPU's copy of the allocation-free GEMM's workspace (device current)
+    void* noalloc = nullptr;
+    TH_HIP(hipGetSymbolAddress(&noalloc, HIP_SYMBOL(scratch)));
     th_device* d = new th_device();
     d->ordinal = ordinal;
+    d->noalloc_scratch = noalloc;
     TH_HIP(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
     TH_HIP(hipEventCreate(&d->ev_start));
     TH_HIP(hipEventCreate(&d->ev_stop));

@@ -128,11 +128,13 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __re
 
 // Convert m activation rows (f32 or bf16, rows of ldx) into the MFMA GEMM's
 // prepared layout in the device's operand workspace.
+size_t prepared_x_bytes(size_t m, size_t Kp) { return round_up(m * Kp * 2, 256) + round_up(m * sizeof(int), 256); }
+
 PreparedX prepare_x(th_device* dev, const void* x, bool xf32, size_t m, size_t ldx, size_t K, size_t Kp,
-                    hipStream_t s, const int* rows) {
+                    hipStream_t s, const int* rows, void* workspace) {
     TH_REQUIRE(m * Kp * 2 < 0x7FFFFFF0u, "prepared activations above 2 GiB");  // 32-bit buffer offsets
     const size_t xbytes = round_up(m * Kp * 2, 256);
-    char* ws = (char*)device_scratch_x(dev, xbytes + m * sizeof(int));
+    char* ws = workspace ? (char*)workspace : (char*)device_scratch_x(dev, prepared_x_bytes(m, Kp));
     PreparedX p{(const uint16_t*)ws, (const int*)(ws + xbytes)};
     if (xf32)
         hipLaunchKernelGGL((q4_gemm_xprep_kernel<true>), dim3((unsigned)m), dim3(256), 0, s, x, (int)ldx, (int)K,
@@ -144,22 +146,33 @@ PreparedX prepare_x(th_device* dev, const void* x, bool xf32, size_t m, size_t l
     return p;
 }
 
+// A caller-provided workspace for the split-K partials (part_bytes of it);
+// with none the device's grow-only workspace is used.
+struct SplitWorkspace {
+    float* part = nullptr;
+    size_t part_bytes = 0;
+};
+
 template <int RT, int CB, typename ST>
 static void q4_mfma_launch(const th_qweight* w, PreparedX xp, size_t m, float* y, size_t ldy, hipStream_t s,
-                           th_device* dev, bool accumulate = false) {
+                           th_device* dev, bool accumulate, SplitWorkspace sw) {
     const size_t NT = w->Np / 16, GQ = w->Kp / 128;
     const unsigned gx = (unsigned)ceil_div(NT, 4 * RT);
     const unsigned gy = (unsigned)ceil_div(m, 16 * CB);
-    // Split K so that the grid covers the chip at least twice.
+    // Split K so that the grid covers the chip at least twice (and, with a
+    // caller's workspace, only as far as its partials fit).
     const size_t target = 2 * (size_t)(dev ? dev->num_cus : 256);
+    const size_t part_row = m * w->rows * sizeof(float);
     size_t ks = 1;
-    while ((size_t)gx * gy * ks < target && ks * 2 <= GQ && ks < 16) ks *= 2;
+    while ((size_t)gx * gy * ks < target && ks * 2 <= GQ && ks < 16 &&
+           (!sw.part || ks * 2 * part_row <= sw.part_bytes))
+        ks *= 2;
     const int gps = (int)ceil_div(GQ, ks);
     ks = ceil_div(GQ, (size_t)gps);
     float* out = y;
     int ldo = (int)ldy;
     if (ks > 1) {
-        out = (float*)device_scratch(dev, ks * m * w->rows * sizeof(float));
+        out = sw.part ? sw.part : (float*)device_scratch(dev, ks * part_row);
         ldo = (int)w->rows;
     }
     GemmDense src;
@@ -183,15 +196,17 @@ static void q4_mfma_launch(const th_qweight* w, PreparedX xp, size_t m, float* y
 // 2x8, 4x4, 4x8).
 template <typename ST>
 static void q4_mfma_dispatch(const th_qweight* w, PreparedX xp, size_t m, float* y, size_t ldy, hipStream_t s,
-                             th_device* dev, bool accumulate) {
-    if (m <= 16) q4_mfma_launch<1, 1, ST>(w, xp, m, y, ldy, s, dev, accumulate);
-    else if (m <= 1024) q4_mfma_launch<2, 4, ST>(w, xp, m, y, ldy, s, dev, accumulate);
-    else q4_mfma_launch<2, 8, ST>(w, xp, m, y, ldy, s, dev, accumulate);
+                             th_device* dev, bool accumulate, SplitWorkspace sw = SplitWorkspace{}) {
+    if (m <= 16) q4_mfma_launch<1, 1, ST>(w, xp, m, y, ldy, s, dev, accumulate, sw);
+    else if (m <= 1024) q4_mfma_launch<2, 4, ST>(w, xp, m, y, ldy, s, dev, accumulate, sw);
+    else q4_mfma_launch<2, 8, ST>(w, xp, m, y, ldy, s, dev, accumulate, sw);
 }
 
+// ws (optional, ws_bytes long): the caller's workspace for the MFMA path's
+// prepared activations followed by its split-K partials.
 template <bool XF32, typename ST>
 static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
-                        hipStream_t s, th_device* dev) {
+                        hipStream_t s, th_device* dev, void* ws = nullptr, size_t ws_bytes = 0) {
     const int GQ = (int)(w->Kp / 128), cus = dev && dev->num_cus > 0 ? dev->num_cus : 256;
     const bool fits8 = Q4GemvSmem<8, 8>::bytes(GQ) <= 160 * 1024;    // staged rows fit LDS
     const bool fits16 = Q4GemvSmem<16, 16>::bytes(GQ) <= 160 * 1024;
@@ -201,8 +216,17 @@ static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx
     else if (!XF32 && m <= 8 && fits8) q4_span_launch<8, false, ST>(w, x, m, ldx, y, ldy, s, cus);
     else if (!XF32 && m <= 16 && fits16) q4_span_launch<16, false, ST>(w, x, m, ldx, y, ldy, s, cus);
     else {  // activations prepared once per call, then the MFMA GEMM
-        const PreparedX xp = prepare_x(dev, x, XF32, m, ldx, w->cols, w->Kp, s, nullptr);
-        q4_mfma_dispatch<ST>(w, xp, m, y, ldy, s, dev, false);
+        SplitWorkspace sw;
+        void* xws = nullptr;
+        if (ws) {
+            const size_t xb = prepared_x_bytes(m, w->Kp);
+            TH_REQUIRE(xb <= ws_bytes, "workspace too small for the prepared activations (m x K too large)");
+            xws = ws;
+            sw.part = (float*)((char*)ws + xb);
+            sw.part_bytes = ws_bytes - xb;
+        }
+        const PreparedX xp = prepare_x(dev, x, XF32, m, ldx, w->cols, w->Kp, s, nullptr, xws);
+        q4_mfma_dispatch<ST>(w, xp, m, y, ldy, s, dev, false, sw);
     }
 }
 
@@ -215,17 +239,17 @@ void launch_q4_linear_prepared(const th_qweight* w, PreparedX xp, size_t m, floa
 }
 
 void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m, size_t ldx, float* y,
-                      size_t ldy, hipStream_t s, th_device* dev) {
+                      size_t ldy, hipStream_t s, th_device* dev, void* ws, size_t ws_bytes) {
     TH_REQUIRE(w && w->bits == 4, "not a q4 weight");
     TH_REQUIRE(xdt == TH_F32 || xdt == TH_BF16, "activations must be f32 or bf16");
     if (m == 0) return;
     const bool f32 = xdt == TH_F32;
     if (w->scale_dtype == TH_F16) {
-        if (f32) q4_linear_t<true, _Float16>(w, x, m, ldx, y, ldy, s, dev);
-        else q4_linear_t<false, _Float16>(w, x, m, ldx, y, ldy, s, dev);
+        if (f32) q4_linear_t<true, _Float16>(w, x, m, ldx, y, ldy, s, dev, ws, ws_bytes);
+        else q4_linear_t<false, _Float16>(w, x, m, ldx, y, ldy, s, dev, ws, ws_bytes);
     } else {
-        if (f32) q4_linear_t<true, float>(w, x, m, ldx, y, ldy, s, dev);
-        else q4_linear_t<false, float>(w, x, m, ldx, y, ldy, s, dev);
+        if (f32) q4_linear_t<true, float>(w, x, m, ldx, y, ldy, s, dev, ws, ws_bytes);
+        else q4_linear_t<false, float>(w, x, m, ldx, y, ldy, s, dev, ws, ws_bytes);
     }
 }
 
@@ -291,6 +315,18 @@ int th_gemm_q4(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w
     require_len_any(x, m * w->cols, "x");
     require_len(y, TH_F32, m * w->rows, "y");
     launch_q4_linear(w, x->ptr, x->dtype, m, w->cols, (float*)y->ptr, w->rows, dev->stream, dev);
+    TH_API_END
+}
+
+int th_gemm_q4_noalloc(th_device* dev, const th_buffer* x, size_t m, const th_qweight* w, th_buffer* y) {
+    TH_API_BEGIN
+    TH_REQUIRE(dev && x && w && y, "null argument");
+    TH_REQUIRE(w->bits == 4, "weight is not q4");
+    TH_REQUIRE(dev->noalloc_scratch, "no workspace address for this device");
+    require_len_any(x, m * w->cols, "x");
+    require_len(y, TH_F32, m * w->rows, "y");
+    launch_q4_linear(w, x->ptr, x->dtype, m, w->cols, (float*)y->ptr, w->rows, dev->stream, dev, dev->noalloc_scratch,
+                     TH_NOALLOC_SCRATCH_BYTES);
     TH_API_END
 }
 

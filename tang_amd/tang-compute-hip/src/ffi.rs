@@ -24,6 +24,9 @@ pub const TH_I8: c_int = 4;
 pub const TH_U32: c_int = 5;
 pub const TH_I32: c_int = 6;
 
+/// Size of the per-GPU workspace of `th_gemm_q4_noalloc`.
+pub const TH_NOALLOC_SCRATCH_BYTES: usize = 64 << 20;
+
 // safetensors dtypes (th_st_info)
 pub const TH_ST_F64: c_int = 0;
 pub const TH_ST_F32: c_int = 1;
@@ -145,6 +148,7 @@ extern "C" {
     pub fn th_st_upload_q8(dev: *mut th_device, f: *const th_st_file, name: *const c_char, out: *mut *mut th_qweight) -> c_int;
     pub fn th_gemm_q4(dev: *mut th_device, x: *const th_buffer, m: usize, w: *const th_qweight, y: *mut th_buffer) -> c_int;
     pub fn th_gemv_q8(dev: *mut th_device, x: *const th_buffer, m: usize, w: *const th_qweight, y: *mut th_buffer) -> c_int;
+    pub fn th_gemm_q4_noalloc(dev: *mut th_device, x: *const th_buffer, m: usize, w: *const th_qweight, y: *mut th_buffer) -> c_int;
     pub fn th_bench_linear(dev: *mut th_device, x: *const th_buffer, m: usize, ws: *const *mut th_qweight, n_w: usize, y: *mut th_buffer, iters: usize, use_graph: c_int, ms: *mut f32) -> c_int;
     pub fn th_matmul_ex(dev: *mut th_device, a: *const th_buffer, b: *const th_buffer, m: usize, k: usize, n: usize, trans_a: c_int, trans_b: c_int, accumulate: c_int, c: *mut th_buffer) -> c_int;
     pub fn th_matmul(dev: *mut th_device, a: *const th_buffer, b: *const th_buffer, m: usize, k: usize, n: usize, c: *mut th_buffer) -> c_int;
