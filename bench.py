@@ -9,7 +9,9 @@ the weights stream from HBM, not the 256 MB Infinity Cache.  Times come from
 HIP events recorded on the library's own stream (th_bench_linear,
 th_llama_time_steps).  The CPU baseline is the oracle's restatement of the
 reference q4_matvec (crates/tang-infer/src/quantize.rs:256-289), f64,
-single thread, on a bounded sample of the same workload.
+single thread, on a bounded sample of the same workload
+(`cpu_baseline`), and the same restatement on every other config, one core
+and all cores (`cpu_baselines_all_configs`, with the CPU model and nproc).
 
 Prints ONE JSON line.
 """
@@ -237,6 +239,99 @@ def cpu_baseline(budget_s=12.0, threads=1):
                        % (calls, rows, N, dt, us))
 
 
+def _timed(fn, budget_s, min_calls=1):
+    """Calls fn until budget_s has passed (at least min_calls); seconds per call."""
+    calls, t0 = 0, time.time()
+    while calls < min_calls or time.time() - t0 < budget_s:
+        fn()
+        calls += 1
+    return (time.time() - t0) / calls, calls
+
+
+def cpu_config1(threads):
+    """Config 1 on the oracle's q8_matvec (f64, serial per row)."""
+    import oracle
+    q, rs = capi.synth_q8_rowwise(1, 4096, 4096)
+    x = capi.synth_normal(11, 4096, 1.0, capi.F32).astype(np.float64)
+    scales = np.repeat(rs[:, None], 128, axis=1)
+    sec, calls = _timed(lambda: oracle.q8_matvec_soa(q, scales, 4096, 4096, x, threads=threads), 3.0)
+    return dict(us_per_call=round(sec * 1e6, 1), cores=threads, sample="%d full calls" % calls)
+
+
+def cpu_config3(threads):
+    """Config 3 decode step on the oracle (or_llama_decode_step at position
+    2048, KV prefilled to 2048): the 7B step is timed by layers, as
+    per-layer = t(2 layers) - t(1 layer) and s/token = t(1 layer) +
+    31 per-layer (the LM head and embedding are in both samples)."""
+    from oracle.models import CONFIG_7B, OracleLlama
+    t = {}
+    for n_layers in (1, 2):
+        cfg = dict(CONFIG_7B, n_layers=n_layers)
+        ref = OracleLlama(cfg, 3, 33, 2048)
+        best = None
+        for _ in range(2):
+            t0 = time.time()
+            ref.step(10, 2048, threads=threads)
+            dt = time.time() - t0
+            best = dt if best is None else min(best, dt)
+        t[n_layers] = best
+        del ref
+    per_layer = t[2] - t[1]
+    s_tok = t[1] + 31 * per_layer
+    return dict(s_per_token=round(s_tok, 3), cores=threads,
+                sample="one step each with 1 and 2 layers (%.2f s, %.2f s; best of 2): %.3f s per layer"
+                       % (t[1], t[2], per_layer))
+
+
+def cpu_config4(threads, T, sample_tokens):
+    """Config 4 MoE layer on the oracle (or_moe_forward, per token
+    independent): sample_tokens of the T-token batch, scaled to T."""
+    from oracle.models import CONFIG4, OracleMoe
+    ref = OracleMoe(CONFIG4, 4)
+    h = capi.synth_normal(45, sample_tokens * CONFIG4["d"], 1.0, capi.BF16)
+    sec, calls = _timed(lambda: ref.forward(h, sample_tokens, threads=threads), 2.0)
+    return dict(T=T, us_per_call=round(sec * T / sample_tokens * 1e6, 1), cores=threads,
+                sample="%d calls on %d of the %d tokens" % (calls, sample_tokens, T))
+
+
+def cpu_config5(threads):
+    """Config 5 absorbed MLA decode on the oracle (or_mla_decode), B=8 x
+    4096 positions."""
+    import oracle
+    c = MLA
+    B, H, Lk, dn, dr, r, dv = c["B"], c["H"], c["L"], c["dn"], c["dr"], c["r"], c["dv"]
+    qn = capi.synth_normal(1, B * H * dn, 1.0, capi.F32)
+    qr = capi.synth_normal(2, B * H * dr, 1.0, capi.F32)
+    cache = capi.synth_normal(3, B * Lk * (r + dr), 1.0, capi.BF16)
+    wuk, suk = capi.synth_q8_rowwise(4, H * r, dn)
+    wuv, suv = capi.synth_q8_rowwise(5, H * dv, r)
+    sec, calls = _timed(lambda: oracle.mla_decode(qn, qr, cache, B, H, Lk, dn, dr, r, dv, wuk, suk, wuv, suv,
+                                                  1.0 / np.sqrt(dn + dr), threads=threads), 2.0)
+    return dict(us_per_call=round(sec * 1e6, 1), cores=threads, sample="%d full calls" % calls)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_suite(threads_all):
+    """The reference CPU path on the host cores for every config, one core
+    (the reference is serial) and, where a sample allows, all cores."""
+    return dict(
+        cpu_model=cpu_model(), nproc=os.cpu_count(), threads_used=threads_all,
+        config1_q8_gemv=[cpu_config1(1), cpu_config1(threads_all)],
+        config3_decode_7b=[cpu_config3(1), cpu_config3(threads_all)],
+        config4_moe=[cpu_config4(1, 16, 16), cpu_config4(threads_all, 512, 64)],
+        config5_mla=[cpu_config5(1), cpu_config5(threads_all)],
+    )
+
+
 def cpu_threads():
     """Host threads for the parallel baseline: the OpenMP setting if any (the
     GPU hosts set it to the job's CPU share), else the visible cores."""
@@ -294,6 +389,7 @@ def main():
     mla = None if args.no_moe_mla else mla_bench(dev, 400)
     cpu = None if args.no_cpu else cpu_baseline()
     cpu_par = None if args.no_cpu else cpu_baseline(6.0, cpu_threads())
+    cpu_all = None if args.no_cpu else cpu_suite(cpu_threads())
     out = {
         "metric": METRIC,
         "value": round(gbs, 1),
@@ -317,6 +413,7 @@ def main():
                      "traffic_source": "profiles/q4_gemv_config2.md (FETCH_SIZE/WRITE_SIZE, copy-calibrated)"},
         "cpu_baseline": cpu,
         "cpu_baseline_parallel": cpu_par,
+        "cpu_baselines_all_configs": cpu_all,
         "q8_config1": q8,
         "prefill_gemm_config2_matrix": prefill,
         "decode_7b": decode,
