@@ -393,7 +393,10 @@ inline void launch_attn_prefill(const float* q, int ldq, const _Float16* kc, con
 // for every position); splits past it only write an empty record.  (Sharing
 // the length evenly over all n_splits workgroups was measured slower: more
 // workgroups each paying the record and merge overhead.)
-template <int D, int SPL, bool OUT_BF16, int NT>
+// EVEN: the attended length is shared evenly over the n_splits workgroups
+// (ceil(attend / n_splits) <= SPL positions each, so every workgroup of the
+// launch streams the same bytes) instead of fixed SPL-position chunks.
+template <int D, int SPL, bool OUT_BF16, int NT, bool EVEN = false>
 __global__ __launch_bounds__(NT) void attn_decode_kernel(const float* __restrict__ q, const _Float16* __restrict__ kc,
                                                           const _Float16* __restrict__ vc, int n_heads, int n_kv_heads,
                                                           int n_splits, float* __restrict__ part,
@@ -413,8 +416,9 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(const float* __restrict
     const int kv_dim = n_kv_heads * D;
     const int kv_h = h / (n_heads / n_kv_heads);
     const int attend = *cache_start_dev + 1;  // <= n_splits * SPL (checked by the host)
-    const int j0 = s * SPL;
-    const int len = max(0, min(SPL, attend - j0));
+    const int per = EVEN ? (attend + n_splits - 1) / n_splits : SPL;  // <= SPL
+    const int j0 = s * per;
+    const int len = max(0, min(per, attend - j0));
     float* recs = part + (size_t)h * n_splits * (D + 2);
     float* rec = recs + (size_t)s * (D + 2);
     if (len == 0) {
@@ -504,7 +508,7 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(const float* __restrict
     // splits that hold keys (the others wrote empty records), sixteen splits
     // per round of coherent loads, with a running max; every thread forms
     // the same M and L in the same order.
-    const int ns = min(n_splits, (attend + SPL - 1) / SPL);
+    const int ns = min(n_splits, (attend + per - 1) / per);
     const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(recs, (uint32_t)(ns * (D + 2)) * 4u);
     for (int d = tid; d < D; d += NT) {
         float M = -INFINITY, L = 0.0f, A = 0.0f;
@@ -585,7 +589,7 @@ inline void launch_attn_split(const float* q, const void* kc, const void* vc, bo
 
 // Decode attention for the engine: one query, f16 cache, SPL positions per
 // split; counters (n_heads ints) zero on entry and on return.
-template <int SPL, bool OUT_BF16, int NT = 256>
+template <int SPL, bool OUT_BF16, int NT = 256, bool EVEN = false>
 inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float16* vc, int n_heads, int n_kv_heads,
                                int head_dim, int n_splits, float* part, int* counters, void* out,
                                const int* cache_start_dev, hipStream_t s) {
@@ -593,9 +597,9 @@ inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float1
     const dim3 grid((unsigned)n_heads, 1, (unsigned)n_splits);
     const size_t lds = 0;
     switch (head_dim) {
-        case 64: hipLaunchKernelGGL((attn_decode_kernel<64, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 128: hipLaunchKernelGGL((attn_decode_kernel<128, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 256: hipLaunchKernelGGL((attn_decode_kernel<256, SPL, OUT_BF16, NT>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 64: hipLaunchKernelGGL((attn_decode_kernel<64, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 128: hipLaunchKernelGGL((attn_decode_kernel<128, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 256: hipLaunchKernelGGL((attn_decode_kernel<256, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
         default: throw Error(TH_ERR_INVALID, "launch_attn_decode: unsupported head_dim");
     }
     TH_LAUNCH_CHECK();

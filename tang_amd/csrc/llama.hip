@@ -34,7 +34,11 @@ enum : int { T_WQ = 0, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_ATTN_NORM, T_FFN_NO
              T_EMBED = 10, T_FINAL_NORM, T_LM_HEAD, T_KCACHE = 20, T_VCACHE };
 
 constexpr float Q4_SMIN = 0.002f, Q4_SMAX = 0.01f, NORM_STD = 0.02f;
-constexpr int ATTN_SPLIT_ENGINE = 256;  // cache positions per attention workgroup
+constexpr int ATTN_SPLIT_ENGINE = 256;  // cache positions per attention workgroup (fixed-chunk mode)
+// Even mode: the attended length shared over n_heads * n_splits workgroups,
+// n_splits = CUs / n_heads (one round of the chip), at most ATTN_EVEN_MAX
+// positions per workgroup; ATTN_EVEN_MAX is the largest instantiated bound.
+constexpr int ATTN_EVEN_SPLS[] = {128, 192, 256, 288, 384, 512};
 
 // state[0] = position, state[1] = current token, state[2] = steps taken
 struct LlamaState { int pos, token, step, pad; };
@@ -410,6 +414,8 @@ struct th_llama {
     th_device* dev = nullptr;
     th_llama_config cfg{};
     int qd = 0, kvd = 0, max_steps = 0, n_splits = 0;
+    bool attn_even = true;  // decode attention splits: even shares of the attended length
+    int attn_spl = 0;       // even mode: positions per workgroup at most (an ATTN_EVEN_SPLS entry)
     std::vector<th_qweight*> wqkv, wo, wgu, wd;
     th_qweight* lm = nullptr;
     uint16_t *embed = nullptr, *attn_norm = nullptr, *ffn_norm = nullptr, *final_norm = nullptr;
@@ -458,6 +464,30 @@ static T* dalloc(size_t n) {
 }
 
 // Enqueue one decode step (all layers) on the device stream.
+
+// The engine's decode attention: even splits (attn_spl positions at most per
+// workgroup) or fixed ATTN_SPLIT_ENGINE-position chunks.
+static void launch_engine_attention(th_llama* m, const _Float16* kc, const _Float16* vc, hipStream_t s) {
+    const th_llama_config& c = m->cfg;
+    const int hd = c.head_dim;
+    const int* pos = (const int*)&m->st->pos;
+    if (!m->attn_even) {
+        launch_attn_decode<ATTN_SPLIT_ENGINE, true>(m->q, kc, vc, c.n_heads, c.n_kv_heads, hd, m->n_splits, m->part,
+                                                    m->counters, (void*)m->att, pos, s);
+        return;
+    }
+#define TH_ATT_EVEN(S)                                                                                                \
+    case S:                                                                                                           \
+        launch_attn_decode<S, true, 256, true>(m->q, kc, vc, c.n_heads, c.n_kv_heads, hd, m->n_splits, m->part,       \
+                                               m->counters, (void*)m->att, pos, s);                                   \
+        break;
+    switch (m->attn_spl) {
+        TH_ATT_EVEN(128) TH_ATT_EVEN(192) TH_ATT_EVEN(256) TH_ATT_EVEN(288) TH_ATT_EVEN(384) TH_ATT_EVEN(512)
+        default: throw Error(TH_ERR_INVALID, "attention split size not instantiated");
+    }
+#undef TH_ATT_EVEN
+}
+
 static void llama_enqueue_step(th_llama* m) {
     const th_llama_config& c = m->cfg;
     hipStream_t s = m->dev->stream;
@@ -474,8 +504,7 @@ static void llama_enqueue_step(th_llama* m) {
         an.ssq = m->ssq; an.nssq = nssq; an.w = m->attn_norm + (size_t)l * d; an.eps = c.eps;
         gemv_engine<true>(m->wqkv[l], m->x, an,
                           EpiQKV{{}, m->q, kc, vc, m->rope_cos, m->rope_sin, m->st, m->qd, m->kvd, hd}, s);
-        launch_attn_decode<ATTN_SPLIT_ENGINE, true>(m->q, kc, vc, c.n_heads, c.n_kv_heads, hd, m->n_splits, m->part,
-                                                    m->counters, (void*)m->att, (const int*)&m->st->pos, s);
+        launch_engine_attention(m, kc, vc, s);
         gemv_engine<false>(m->wo[l], m->att, NormArgs{}, EpiAddToSsq{m->x, m->ssq}, s);
         NormArgs fn;
         fn.ssq = m->ssq; fn.nssq = nssq; fn.w = m->ffn_norm + (size_t)l * d; fn.eps = c.eps;
@@ -729,7 +758,25 @@ int th_llama_create(th_device* dev, const th_llama_config* cfg, th_llama** out) 
         m->qd = c.n_heads * c.head_dim;
         m->kvd = c.n_kv_heads * c.head_dim;
         m->max_steps = c.max_seq;
-        m->n_splits = (int)ceil_div((size_t)c.max_seq, ATTN_SPLIT_ENGINE);
+        // even splits: one workgroup per CU (n_heads * n_splits ~ CUs), each
+        // at most attn_spl positions; TANG_HIP_ATTN_FIXED=1 selects fixed
+        // ATTN_SPLIT_ENGINE-position chunks instead
+        const char* fixed = getenv("TANG_HIP_ATTN_FIXED");
+        m->attn_even = !(fixed && fixed[0] == '1');
+        if (m->attn_even) {
+            const int want = std::max(1, dev->num_cus / c.n_heads);
+            const int need = (int)ceil_div((size_t)c.max_seq, (size_t)want);
+            m->attn_spl = ATTN_EVEN_SPLS[sizeof(ATTN_EVEN_SPLS) / sizeof(int) - 1];
+            for (int v : ATTN_EVEN_SPLS)
+                if (v >= need) { m->attn_spl = v; break; }
+            m->n_splits = (int)ceil_div((size_t)c.max_seq, (size_t)m->attn_spl);
+            // spread over the same split count as the request, or more when
+            // the largest split size caps it
+            m->n_splits = std::max(m->n_splits, std::min(want, (int)ceil_div((size_t)c.max_seq, (size_t)64)));
+            TH_REQUIRE(m->n_splits <= 256, "max_seq too long for the attention splits");
+        } else {
+            m->n_splits = (int)ceil_div((size_t)c.max_seq, ATTN_SPLIT_ENGINE);
+        }
         TH_HIP(hipSetDevice(dev->ordinal));
         const size_t L = c.n_layers, d = c.d_model;
         m->embed = dalloc<uint16_t>((size_t)c.vocab * d);
