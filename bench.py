@@ -352,6 +352,8 @@ def main():
     ap.add_argument("--no-moe-mla", action="store_true")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="counter runs: 240 GEMV launches, then one 256 MiB device copy as the traffic calibration")
+    ap.add_argument("--profile-m", type=int, default=0,
+                    help="counter runs: 240 stream-launched config-2 GEMVs at this batch size")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="counter runs: four M=2048 prefill GEMMs on the config-2 matrix")
     args = ap.parse_args()
@@ -361,6 +363,10 @@ def main():
         sys.exit(2)
 
     dev = capi.HipComputeDevice(0)
+    if args.profile_m:
+        gemv_bench(dev, args.profile_m, 240, 0, graph=False)
+        print(json.dumps({"profile_m": args.profile_m, "launches": 240}))
+        return
     if args.profile_gemm:
         print(json.dumps(prefill_bench(dev, 2048, steps=4)))
         return

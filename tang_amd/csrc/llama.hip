@@ -123,8 +123,10 @@ struct EpiSwiGLU : EpiNoFinish {
     }
 };
 
-// LM head: store the logits and each tile's first maximum (tile order and
-// in-tile order keep sampling.rs:184-194's first-index tie rule).
+// LM-head epilogue: logits, and each 16-row tile's maximum (first maximum
+// within the tile) for llama_argmax_embed_kernel.  (Taking the final argmax
+// in the last workgroup to finish was measured slower: its arrival counter
+// sees one atomic per tile, 2000 at the 7B shape, and they serialise.)
 struct EpiTileMax {
     static constexpr bool HAS_FINISH = true;
     float* logits; float* part_v; int* part_i; int vocab;
@@ -145,37 +147,55 @@ struct EpiTileMax {
     }
 };
 
-// Greedy argmax over the tile maxima (first maximum wins), record the token,
-// advance the position.
-__global__ __launch_bounds__(1024) void llama_argmax_kernel(const float* __restrict__ part_v,
-                                                            const int* __restrict__ part_i, int ntile, LlamaState* st,
-                                                            int32_t* __restrict__ history) {
-    __shared__ float rv[1024];
-    __shared__ int ri[1024];
-    const int tid = threadIdx.x;
+// Greedy argmax over the tile maxima (value descending, then index
+// ascending: the first maximum wins, sampling.rs:184-194); records the
+// token, advances the position and writes the next step's input: the
+// token's embedding row into x and its per-16-element sums of squares into
+// ssq (cpu.rs:151-168, as llama_embed_kernel), so a step needs no embedding
+// launch of its own.  One 1024-thread workgroup; d <= 16384.
+__global__ __launch_bounds__(1024) void llama_argmax_embed_kernel(const float* __restrict__ part_v,
+                                                                  const int* __restrict__ part_i, int ntile,
+                                                                  LlamaState* st, int32_t* __restrict__ history,
+                                                                  const uint16_t* __restrict__ embed, int d,
+                                                                  float* __restrict__ x, float* __restrict__ ssq) {
+    __shared__ float wv[16];
+    __shared__ int wi[16], s_tok;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = tid; i < ntile; i += 1024) {
+    for (int i = tid; i < ntile; i += 1024) {  // ascending i: strict > keeps the first
         const float pv = part_v[i];
         if (pv > bv) { bv = pv; bi = part_i[i]; }
     }
-    rv[tid] = bv;
-    ri[tid] = bi;
-    __syncthreads();
-    for (int s = 512; s > 0; s >>= 1) {
-        if (tid < s) {
-            const float ov = rv[tid + s];
-            const int oi = ri[tid + s];
-            if (ov > rv[tid] || (ov == rv[tid] && oi < ri[tid])) { rv[tid] = ov; ri[tid] = oi; }
-        }
-        __syncthreads();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
     }
+    if (lane == 0) { wv[wave] = bv; wi[wave] = bi; }
+    __syncthreads();
     if (tid == 0) {
-        const int tok = ri[0] == 0x7fffffff ? 0 : ri[0];
+        for (int w = 1; w < 16; w++)
+            if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) { bv = wv[w]; bi = wi[w]; }
+        const int tok = bi == 0x7fffffff ? 0 : bi;
         history[st->step] = tok;
         st->token = tok;
         st->step += 1;
         st->pos += 1;
+        s_tok = tok;
+    }
+    __syncthreads();
+    const uint16_t* src = embed + (size_t)s_tok * d;
+    for (int c = tid; c * 16 < d; c += 1024) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float v = __uint_as_float((uint32_t)src[c * 16 + i] << 16);
+            x[c * 16 + i] = v;
+            sq += v * v;
+        }
+        ssq[c] = sq;
     }
 }
 
@@ -465,6 +485,28 @@ static T* dalloc(size_t n) {
 
 // Enqueue one decode step (all layers) on the device stream.
 
+// Final RMSNorm and LM head (tile maxima), then the greedy argmax, which
+// also writes the next token's embedding.
+static void llama_lm_head_argmax(th_llama* m, hipStream_t s) {
+    const th_llama_config& c = m->cfg;
+    const int d = c.d_model;
+    NormArgs fin;
+    fin.ssq = m->ssq; fin.nssq = d / 16; fin.w = m->final_norm; fin.eps = c.eps;
+    gemv_engine<true>(m->lm, m->x, fin, EpiTileMax{m->logits, m->amax_v, m->amax_i, c.vocab}, s);
+    hipLaunchKernelGGL(llama_argmax_embed_kernel, dim3(1), dim3(1024), 0, s, m->amax_v, m->amax_i,
+                       (int)ceil_div((size_t)c.vocab, 16), m->st, m->history, m->embed, d, m->x, m->ssq);
+    TH_LAUNCH_CHECK();
+}
+
+// x / ssq <- the embedding of the state's current token (after the host
+// sets the token; decode steps chain it themselves).
+static void llama_embed_current(th_llama* m, hipStream_t s) {
+    const int d = m->cfg.d_model;
+    hipLaunchKernelGGL(llama_embed_kernel, dim3((unsigned)ceil_div((size_t)d / 16, (size_t)256)), dim3(256), 0, s,
+                       m->embed, m->st, d, m->x, m->ssq);
+    TH_LAUNCH_CHECK();
+}
+
 // The engine's decode attention: even splits (attn_spl positions at most per
 // workgroup) or fixed ATTN_SPLIT_ENGINE-position chunks.
 static void launch_engine_attention(th_llama* m, const _Float16* kc, const _Float16* vc, hipStream_t s) {
@@ -493,9 +535,8 @@ static void llama_enqueue_step(th_llama* m) {
     hipStream_t s = m->dev->stream;
     const int d = c.d_model, hd = c.head_dim;
     const int nssq = d / 16;
-    hipLaunchKernelGGL(llama_embed_kernel, dim3((unsigned)ceil_div(nssq, 256)), dim3(256), 0, s, m->embed, m->st, d, m->x,
-                       m->ssq);
-    TH_LAUNCH_CHECK();
+    // x and ssq hold the current token's embedding: written by the previous
+    // step's argmax (llama_argmax_embed_kernel) or by llama_embed_current
     const size_t cache_layer = (size_t)c.max_seq * m->kvd;
     for (int l = 0; l < c.n_layers; l++) {
         _Float16* kc = m->kcache + l * cache_layer;
@@ -511,12 +552,7 @@ static void llama_enqueue_step(th_llama* m) {
         gemv_engine<true>(m->wgu[l], m->x, fn, EpiSwiGLU{{}, m->sg}, s);
         gemv_engine<false>(m->wd[l], m->sg, NormArgs{}, EpiAddToSsq{m->x, m->ssq}, s);
     }
-    NormArgs fin;
-    fin.ssq = m->ssq; fin.nssq = nssq; fin.w = m->final_norm; fin.eps = c.eps;
-    gemv_engine<true>(m->lm, m->x, fin, EpiTileMax{m->logits, m->amax_v, m->amax_i, c.vocab}, s);
-    hipLaunchKernelGGL(llama_argmax_kernel, dim3(1), dim3(1024), 0, s, m->amax_v, m->amax_i,
-                       (int)ceil_div((size_t)c.vocab, 16), m->st, m->history);
-    TH_LAUNCH_CHECK();
+    llama_lm_head_argmax(m, s);
 }
 
 static void llama_build_graph(th_llama* m) {
@@ -966,6 +1002,7 @@ int th_llama_set_token(th_llama* m, int32_t token) {
     TH_HIP(hipMemcpy(&s, m->st, sizeof s, hipMemcpyDeviceToHost));
     s.token = token;
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    llama_embed_current(m, m->dev->stream);
     TH_API_END
 }
 
@@ -979,6 +1016,7 @@ int th_llama_step_device(th_llama* m, size_t pos) {
     s.pos = (int)pos;
     s.step = 0;
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    llama_embed_current(m, m->dev->stream);
     llama_launch_step(m);
     TH_API_END
 }
@@ -993,6 +1031,7 @@ int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, in
     LlamaState s{(int)pos, token, 0, 0};
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    llama_embed_current(m, m->dev->stream);
     for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     if (tokens_out) TH_HIP(hipMemcpy(tokens_out, m->history, n_steps * 4, hipMemcpyDeviceToHost));
@@ -1016,6 +1055,7 @@ int th_llama_generate_sampled(th_llama* m, th_sampler* smp, const int32_t* promp
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     TH_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
     hipStream_t s = m->dev->stream;  // non-blocking: every copy goes on it and is waited for
+    llama_embed_current(m, s);
     for (size_t i = 0; i < c.max_tokens; i++) {
         llama_launch_step(m);  // advances the device position; its greedy token is replaced below
         TH_HIP(hipMemcpyAsync(logits.data(), m->logits, logits.size() * 4, hipMemcpyDeviceToHost, s));
@@ -1026,6 +1066,7 @@ int th_llama_generate_sampled(th_llama* m, th_sampler* smp, const int32_t* promp
         past.push_back(next);
         tokens_out[(*n_out)++] = next;
         TH_HIP(hipMemcpyAsync(&m->st->token, &next, sizeof next, hipMemcpyHostToDevice, s));
+        llama_embed_current(m, s);  // the sampled token replaces the greedy one the step embedded
         TH_HIP(hipStreamSynchronize(s));
     }
     TH_API_END
@@ -1053,12 +1094,7 @@ int th_llama_prefill(th_llama* m, const int32_t* tokens, size_t n, size_t pos, i
     hipLaunchKernelGGL(prefill_last_row_kernel, dim3((unsigned)ceil_div((size_t)d / 16, (size_t)256)), dim3(256), 0, s,
                        m->pf_x + (rows - 1) * (size_t)d, d, m->x, m->ssq);
     TH_LAUNCH_CHECK();
-    NormArgs fin;
-    fin.ssq = m->ssq; fin.nssq = d / 16; fin.w = m->final_norm; fin.eps = c.eps;
-    gemv_engine<true>(m->lm, m->x, fin, EpiTileMax{m->logits, m->amax_v, m->amax_i, c.vocab}, s);
-    hipLaunchKernelGGL(llama_argmax_kernel, dim3(1), dim3(1024), 0, s, m->amax_v, m->amax_i,
-                       (int)ceil_div((size_t)c.vocab, 16), m->st, m->history);
-    TH_LAUNCH_CHECK();
+    llama_lm_head_argmax(m, s);
     TH_HIP(hipStreamSynchronize(s));
     if (next_token) TH_HIP(hipMemcpy(next_token, m->history, 4, hipMemcpyDeviceToHost));
     if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost));
@@ -1085,6 +1121,7 @@ int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, 
     LlamaState s{(int)pos, token, 0, 0};
     TH_HIP(hipStreamSynchronize(m->dev->stream));
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
+    llama_embed_current(m, m->dev->stream);
     if (!llama_eager()) llama_build_graph(m);
     TH_HIP(hipEventRecord(m->dev->ev_start, m->dev->stream));
     for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);

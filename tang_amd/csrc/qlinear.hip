@@ -1,4 +1,5 @@
 // Launchers and C entry points for the quantized linear kernels.
+#include <cstdlib>
 #include <map>
 #include <mutex>
 

@@ -78,6 +78,15 @@ __device__ __forceinline__ uint4 ldg_stream(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads()
+// (a workgroup fence over all memory), it does not wait for this wave's
+// outstanding global loads, so weights prefetched before it stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Sum over the 64 lanes in a fixed butterfly order (every lane gets it).
 __device__ __forceinline__ float wave_sum_fixed(float v) {
 #pragma unroll
@@ -541,27 +550,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     // those lanes read real (finite) data of another row: no masking needed.
     const uint4* abase = xw + (size_t)(r < mr_live ? r : 0) * 4 + q;
     const float* cbase = bw + 4 * (q & (BS / 4 - 1));
-    for (int tt = 0; tt < ntl; tt++) {  // one trip unless the source groups tiles
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    auto step = [&](auto refill_tag, int u, int i) {
-        const uint4 wv = wbuf[u];
-        if (u % SI == 0) scur = sbuf[u / SI];  // this record serves items i .. i+SI-1
-        const typename SR::Rec sv = scur;
-        if constexpr (decltype(refill_tag)::value) {
-            if (u % SI == 0) sbuf[u / SI] = *scale_ptr(i + D);
-            wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
-        }
-        if (i >= nmine) return;  // past this wave's items (wave-uniform: a scalar branch)
-        float sj[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) sj[j] = SR::get(sv, u % SI, j);
+    // one item (local index i) of the current tile: four MFMAs (one per
+    // group, bias in C) and the scale FMAs into acc
+    auto item_mfma = [&](int i, const uint4& wv, const float (&sj)[4], float (&acc)[4]) {
         const uint32_t wj[4] = {wv.x, wv.y, wv.z, wv.w};
         const uint4* ai = abase + (size_t)i * 4 * MR * 4;
         const float* ci = cbase + i * 4 * BS;
-        // the four groups' LDS operands are read together and their MFMAs
-        // are independent (the bias rides in C), so one LDS latency and one
-        // MFMA latency cover the item; only the scale FMAs are ordered
         uint4 aq[4];
         float4 cb[4];
 #pragma unroll
@@ -585,59 +579,79 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
             for (int e = 0; e < ACC; e++) acc[e] = __builtin_fmaf(sj[j], d[j][e], acc[e]);
         }
     };
-    const int nbatch = (nmine + D - 1) / D;
-    for (int bt = 0; bt + 1 < nbatch; bt++) {
+    // cross-wave reduction of one tile's partial sums and its epilogue
+    // trailing: a barrier after it (another tile follows in this workgroup)
+    auto tile_end = [&](int tile, const float (&acc)[4], bool trailing) {
+        // lane (q, r) holds D rows 4q..4q+3 of column r
+        if (q * 4 < MR) {
 #pragma unroll
-        for (int u = 0; u < D; u++) step(std::true_type{}, u, bt * D + u);
-    }
-    if (nbatch > 0) {
-#pragma unroll
-        for (int u = 0; u < D; u++) step(std::false_type{}, u, (nbatch - 1) * D + u);
-    }
-    if constexpr (Src::TPW > 1) {
-        // the next tile's first items stream in during this tile's reduction;
-        // branch-free: the last tile re-reads its own first items (cache hits)
-        const int tn = tt + 1 < ntl ? t + 1 : t;
-        const uint4* wpn = wt + (size_t)tn * GQ * 64 + lane;
-#pragma unroll
-        for (int u = 0; u < D; u++) {
-            if (u % SI == 0) sbuf[u / SI] = *scale_ptr_t(u, tn);
-            wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
+            for (int e = 0; e < ACC; e++)
+                if (4 * q + e < MR) red[(wave * RS + 4 * q + e) * 16 + r] = acc[e];
         }
-    }
-
-    // lane (q, r) holds D rows 4q..4q+3 of column r
-    if (q * 4 < MR) {
+        lds_barrier();
+        float v = 0.0f;
+        if (tid < 16 * M) {
+            const int m = tid >> 4, rr = tid & 15;
 #pragma unroll
-        for (int e = 0; e < ACC; e++)
-            if (4 * q + e < MR) red[(wave * RS + 4 * q + e) * 16 + r] = acc[e];
-    }
-    __syncthreads();
-    float v = 0.0f;
-    if (tid < 16 * M) {
-        const int m = tid >> 4, rr = tid & 15;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            if (XF32) v += red[(w * RS + 2 * m) * 16 + rr] + red[(w * RS + 2 * m + 1) * 16 + rr];
-            else v += red[(w * RS + m) * 16 + rr];
+            for (int w = 0; w < NW; w++) {
+                if (XF32) v += red[(w * RS + 2 * m) * 16 + rr] + red[(w * RS + 2 * m + 1) * 16 + rr];
+                else v += red[(w * RS + m) * 16 + rr];
+            }
+            tilev[m * 16 + rr] = v;
         }
-        tilev[m * 16 + rr] = v;
-    }
-    __syncthreads();
-    if (tid < 16 * M) {
-        const int m = tid >> 4, rr = tid & 15;
-        const int n = t * 16 + rr;
-        if (n < N && m < mrows) epi(src.out_row(m), n, v, tilev + m * 16, aux);
-    }
-    if constexpr (Epi::HAS_FINISH) {
-        __syncthreads();
-        epi.finish(t, (int)gridDim.x, aux, tid);
-    }
-    if constexpr (Src::TPW > 1) {
-        __syncthreads();  // red and tilev are rewritten by the next tile
-        t += 1;
-        wp = wt + (size_t)t * GQ * 64 + lane;
-    }
+        lds_barrier();
+        if (tid < 16 * M) {
+            const int m = tid >> 4, rr = tid & 15;
+            const int n = tile * 16 + rr;
+            if (n < N && m < mrows) epi(src.out_row(m), n, v, tilev + m * 16, aux);
+        }
+        if constexpr (Epi::HAS_FINISH) {
+            lds_barrier();
+            epi.finish(tile, (int)gridDim.x, aux, tid);
+        }
+        if (trailing) lds_barrier();  // red and tilev are rewritten by the next tile
+    };
+    for (int tt = 0; tt < ntl; tt++) {  // one trip unless the source groups tiles
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto step = [&](auto refill_tag, int u, int i) {
+            const uint4 wv = wbuf[u];
+            if (u % SI == 0) scur = sbuf[u / SI];  // this record serves items i .. i+SI-1
+            const typename SR::Rec sv = scur;
+            if constexpr (decltype(refill_tag)::value) {
+                if (u % SI == 0) sbuf[u / SI] = *scale_ptr(i + D);
+                wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
+            }
+            if (i >= nmine) return;  // past this wave's items (wave-uniform: a scalar branch)
+            float sj[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) sj[j] = SR::get(sv, u % SI, j);
+            item_mfma(i, wv, sj, acc);
+        };
+        const int nbatch = (nmine + D - 1) / D;
+        for (int bt = 0; bt + 1 < nbatch; bt++) {
+#pragma unroll
+            for (int u = 0; u < D; u++) step(std::true_type{}, u, bt * D + u);
+        }
+        if (nbatch > 0) {
+#pragma unroll
+            for (int u = 0; u < D; u++) step(std::false_type{}, u, (nbatch - 1) * D + u);
+        }
+        if constexpr (Src::TPW > 1) {
+            // the next tile's first items stream in during this tile's reduction;
+            // branch-free: the last tile re-reads its own first items (cache hits)
+            const int tn = tt + 1 < ntl ? t + 1 : t;
+            const uint4* wpn = wt + (size_t)tn * GQ * 64 + lane;
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                if (u % SI == 0) sbuf[u / SI] = *scale_ptr_t(u, tn);
+                wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
+            }
+        }
+        tile_end(t, acc, Src::TPW > 1);
+        if constexpr (Src::TPW > 1) {
+            t += 1;
+            wp = wt + (size_t)t * GQ * 64 + lane;
+        }
     }  // tiles
 }
 
