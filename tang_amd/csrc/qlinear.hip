@@ -137,12 +137,13 @@ PreparedX prepare_x(th_device* dev, const void* x, bool xf32, size_t m, size_t l
     const size_t xbytes = round_up(m * Kp * 2, 256);
     char* ws = workspace ? (char*)workspace : (char*)device_scratch_x(dev, prepared_x_bytes(m, Kp));
     PreparedX p{(const uint16_t*)ws, (const int*)(ws + xbytes)};
+    const unsigned grid = (unsigned)ceil_div(m, (size_t)4);
     if (xf32)
-        hipLaunchKernelGGL((q4_gemm_xprep_kernel<true>), dim3((unsigned)m), dim3(256), 0, s, x, (int)ldx, (int)K,
-                           (int)Kp, rows, (uint4*)ws, (int*)(ws + xbytes));
+        hipLaunchKernelGGL((q4_gemm_xprep_kernel<true>), dim3(grid), dim3(256), 0, s, x, (int)ldx, (int)K, (int)Kp,
+                           (int)m, rows, (uint4*)ws, (int*)(ws + xbytes));
     else
-        hipLaunchKernelGGL((q4_gemm_xprep_kernel<false>), dim3((unsigned)m), dim3(256), 0, s, x, (int)ldx, (int)K,
-                           (int)Kp, rows, (uint4*)ws, (int*)(ws + xbytes));
+        hipLaunchKernelGGL((q4_gemm_xprep_kernel<false>), dim3(grid), dim3(256), 0, s, x, (int)ldx, (int)K, (int)Kp,
+                           (int)m, rows, (uint4*)ws, (int*)(ws + xbytes));
     TH_LAUNCH_CHECK();
     return p;
 }

@@ -132,10 +132,16 @@ template <int U>
 struct ScaleVec<U, _Float16> {
     uint2 v[U];
     __device__ __forceinline__ void load(const _Float16* p, int u) { v[u] = *(const uint2*)p; }
-    __device__ __forceinline__ float get(int u, int j) const {
+    __device__ __forceinline__ float get(int u, int j) const { return (float)geth(u, j); }
+    __device__ __forceinline__ _Float16 geth(int u, int j) const {
         uint32_t w = (j < 2) ? v[u].x : v[u].y;
         uint16_t h = (j & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFF);
-        return (float)__builtin_bit_cast(_Float16, h);
+        return __builtin_bit_cast(_Float16, h);
+    }
+    // the scale times 2^e as f16 (one v_ldexp_f16; subnormal results exact
+    // to f16's spacing)
+    __device__ __forceinline__ _Float16 get_ldexp(int u, int j, int e) const {
+        return __builtin_amdgcn_ldexph(geth(u, j), e);
     }
 };
 template <int U>
@@ -144,6 +150,10 @@ struct ScaleVec<U, float> {
     __device__ __forceinline__ void load(const float* p, int u) { v[u] = *(const float4*)p; }
     __device__ __forceinline__ float get(int u, int j) const {
         return j == 0 ? v[u].x : j == 1 ? v[u].y : j == 2 ? v[u].z : v[u].w;
+    }
+    // scaled in f32, then rounded to f16 once
+    __device__ __forceinline__ _Float16 get_ldexp(int u, int j, int e) const {
+        return (_Float16)__builtin_amdgcn_ldexpf(get(u, j), e);
     }
 };
 
@@ -859,6 +869,15 @@ __host__ __device__ inline int range_exp(float mx, int top) {
     return E - top;
 }
 constexpr int XPREP_TOP = 13;  // prepared activations: row maximum in [2^12, 2^13)
+
+// Largest magnitude over a 256-thread workgroup (every thread gets it).
+__device__ __forceinline__ float block_absmax256(float v, float* red4) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+}
 constexpr int WSCALE_TOP = 9;  // weight scales: row maximum in [2^8, 2^9)
 
 // Sources of the MFMA GEMM: which weights a workgroup multiplies and which
@@ -897,7 +916,7 @@ struct EpiGemmStore {
     }
 };
 
-// Activations prepared for the MFMA GEMM: one workgroup per row.  Pass 1
+// Activations prepared for the MFMA GEMM: one wave per row.  Pass 1
 // finds the row's largest magnitude, pass 2 writes x * 2^-xexp[row] as f16
 // (RNE; exact for a bf16 input within 2^26 of the row maximum), each 8-value
 // chunk in nibble-pair order (x0,x4,x1,x5,x2,x6,x3,x7), zero past K up to Kp.
@@ -931,34 +950,28 @@ __device__ __forceinline__ void xprep_load8(const void* xin, size_t ldx, int row
     }
 }
 
-// Largest magnitude over a 256-thread workgroup (every thread gets it).
-__device__ __forceinline__ float block_absmax256(float v, float* red4) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
-}
-
 template <bool XF32>
 __global__ __launch_bounds__(256) void q4_gemm_xprep_kernel(const void* __restrict__ xin, int ldx, int K, int Kp,
-                                                            const int* __restrict__ rows, uint4* __restrict__ out,
-                                                            int* __restrict__ xexp) {
-    __shared__ float red4[4];
-    const int r = blockIdx.x;
+                                                            int M, const int* __restrict__ rows,
+                                                            uint4* __restrict__ out, int* __restrict__ xexp) {
+    // one wave per row, four rows per workgroup
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= M) return;  // wave-uniform
     const int row = rows ? rows[r] : r;
     const int cpr = Kp >> 3;
     const bool vec = (ldx & 7) == 0 && (((uintptr_t)xin) & 15) == 0;
     float mx = 0.0f;
-    for (int c = threadIdx.x; c < cpr; c += 256) {
+    for (int c = lane; c < cpr; c += 64) {
         float xv[8];
         xprep_load8<XF32>(xin, (size_t)ldx, row, K, c * 8, vec, xv);
 #pragma unroll
         for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(xv[e]));
     }
-    const int e = range_exp(block_absmax256(mx, red4), XPREP_TOP);
-    if (threadIdx.x == 0) xexp[r] = e;
-    for (int c = threadIdx.x; c < cpr; c += 256) {  // second read: L2 hits
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const int e = range_exp(mx, XPREP_TOP);
+    if (lane == 0) xexp[r] = e;
+    for (int c = lane; c < cpr; c += 64) {  // second read: cache hits
         float xv[8];
         xprep_load8<XF32>(xin, (size_t)ldx, row, K, c * 8, vec, xv);
 #pragma unroll
@@ -1077,7 +1090,7 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
 #pragma unroll
             for (int a = 0; a < RT; a++) {
                 const uint32_t w = j == 0 ? wcur[a].x : j == 1 ? wcur[a].y : j == 2 ? wcur[a].z : wcur[a].w;
-                const _Float16 s = (_Float16)__builtin_amdgcn_ldexpf(scur.get(a, j), wneg[a]);
+                const _Float16 s = scur.get_ldexp(a, j, wneg[a]);
                 const half2_t s2 = {s, s};
                 half2_t p[4];
                 nib_pairs_f16(w, s2, p);
