@@ -404,33 +404,54 @@ struct EpiMoeStore : EpiNoFinish {
     }
 };
 
-// out[t] = sum_r w[t][r] * y[slot(t, r)] + sum_s y[shared slot]: rank order,
-// then shared experts (f32).  The token's slots and weights are loaded once;
-// each thread covers 4 consecutive outputs.
+// out[tk][n..n+3] = sum_r w[tk][r] * y[slot(tk, r)] + sum_s y[shared slot]
+// (rank order, then shared experts, f32).  Every slot row of a round of
+// eight is loaded before the first FMA, so a token pays one memory latency
+// per round rather than one per rank; any number of shared experts.
+__device__ __forceinline__ float4 moe_combine4(const float* __restrict__ y, const int* __restrict__ token_slot,
+                                               const float* __restrict__ topk_w, const int* __restrict__ offsets,
+                                               int tk, int n, int k, int E, int S, int d) {
+    auto load4 = [&](int slot) { return *(const float4*)(y + (size_t)slot * d + n); };
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int r0 = 0; r0 < k; r0 += 8) {
+        float4 v[8];
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {  // past k: re-read the last rank (not used)
+            const int r = min(r0 + u, k - 1);
+            w[u] = topk_w[(size_t)tk * k + r];
+            v[u] = load4(token_slot[tk * k + r]);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (r0 + u < k) {
+                acc.x = __builtin_fmaf(w[u], v[u].x, acc.x);
+                acc.y = __builtin_fmaf(w[u], v[u].y, acc.y);
+                acc.z = __builtin_fmaf(w[u], v[u].z, acc.z);
+                acc.w = __builtin_fmaf(w[u], v[u].w, acc.w);
+            }
+    }
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = load4(offsets[E + min(s0 + u, S - 1)] + tk);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u < S) {
+                acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+            }
+    }
+    return acc;
+}
+
+// Combine: one workgroup per token, each thread four consecutive outputs
+// (moe_combine4).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y, const int* __restrict__ token_slot,
                                                           const float* __restrict__ topk_w, const int* __restrict__ offsets,
                                                           int k, int E, int S, int d, float* __restrict__ out) {
     const int t = blockIdx.x;
-    __shared__ int slot[MOE_MAX_K + 8];
-    __shared__ float wk[MOE_MAX_K];
-    const int tid = threadIdx.x;
-    if (tid < k) { slot[tid] = token_slot[t * k + tid]; wk[tid] = topk_w[(size_t)t * k + tid]; }
-    if (tid >= 64 && tid < 64 + S) slot[MOE_MAX_K + tid - 64] = offsets[E + tid - 64] + t;
-    __syncthreads();
-    for (int n = tid * 4; n < d; n += 1024) {
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int r = 0; r < k; r++) {
-            const float4 v = *(const float4*)(y + (size_t)slot[r] * d + n);
-            const float w = wk[r];
-            acc.x = __builtin_fmaf(w, v.x, acc.x); acc.y = __builtin_fmaf(w, v.y, acc.y);
-            acc.z = __builtin_fmaf(w, v.z, acc.z); acc.w = __builtin_fmaf(w, v.w, acc.w);
-        }
-        for (int s = 0; s < S; s++) {
-            const float4 v = *(const float4*)(y + (size_t)slot[MOE_MAX_K + s] * d + n);
-            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-        }
-        *(float4*)(out + (size_t)t * d + n) = acc;
-    }
+    for (int n = threadIdx.x * 4; n < d; n += 1024)
+        *(float4*)(out + (size_t)t * d + n) = moe_combine4(y, token_slot, topk_w, offsets, t, n, k, E, S, d);
 }
 
 }  // namespace th

@@ -85,3 +85,21 @@ def test_moe_many_experts(dev, T):
     assert np.array_equal(idx, r_idx)
     assert max_abs_rel(w, r_w) < 1e-5
     assert max_abs_rel(out, r_out) < 2e-2
+
+
+@pytest.mark.parametrize("T", [6, 80])  # grouped GEMV / grouped MFMA GEMM
+def test_moe_many_shared_experts(dev, T):
+    """Ten shared experts (more than one load round of the combine) and a
+    top-9 routing (more than eight ranks per token)."""
+    cfg = dict(d=256, ff=64, E=16, S=10, k=9)
+    print(f"moe S=10 k=9 T={T}", flush=True)
+    h = capi.synth_normal(90 + T, T * cfg["d"], 1.0, capi.BF16)
+    ref = OracleMoe(cfg, 13)
+    r_out, r_idx, _ = ref.forward(h, T)
+    m = device_moe(dev, cfg, 13)
+    try:
+        out, idx, _ = device_moe_forward(dev, m, cfg, h, T)
+    finally:
+        capi.lib().th_moe_destroy(m)
+    assert np.array_equal(idx, r_idx)
+    assert max_abs_rel(out, r_out) < 2e-2
