@@ -412,6 +412,9 @@ def main():
         "config": {"workload": "q4 g32 GEMV 11008x4096, M=1, bf16 activations (BASELINE config 2), "
                                "%d rotating weight copies (305 MB > 256 MB MALL), launches replayed as one HIP graph"
                                % N_COPIES,
+                   "timed_launches": args.steps,
+                   "before_timing": "the graph replayed once, then one launch per weight copy in copy order, so "
+                                    "every timed read of a copy is %d launches after its previous one" % N_COPIES,
                    "stream_launched": dict(us=round(us_stream, 3), gbs=round(GEMV_BYTES[1] / us_stream / 1e3, 1)),
                    "M_sweep": extra},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
