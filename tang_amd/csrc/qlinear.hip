@@ -70,14 +70,12 @@ static void q4_gemv_dispatch(const th_qweight* w, const void* x, size_t m, size_
     switch (m) {
         case 1: q4_gemv_launch<1, XF32, ST>(w, x, ldx, y, ldy, s); break;
         case 2: q4_gemv_launch<2, XF32, ST>(w, x, ldx, y, ldy, s); break;
-        case 3: q4_gemv_launch<3, XF32, ST>(w, x, ldx, y, ldy, s); break;
-        case 4: q4_gemv_launch<4, XF32, ST>(w, x, ldx, y, ldy, s); break;
         default: throw Error(TH_ERR_INVALID, "q4 gemv: m out of range");
     }
 }
 
-// M block rows (8 or 16 staged rows after f32 hi/lo splitting), m of them
-// live: NW waves split K, and each workgroup takes ceil(tiles / CUs)
+// M block rows (4, 8 or 16; twice that staged after f32 hi/lo splitting), m
+// of them live: NW waves split K, and each workgroup takes ceil(tiles / CUs)
 // consecutive tiles so that the whole grid is resident at once and the
 // staged activations are read once per workgroup.
 template <int M, bool XF32, typename ST, bool VEC, bool RT>
@@ -95,6 +93,9 @@ static void q4_span_launch_v(const th_qweight* w, const void* x, size_t m, size_
     const size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w->Kp / 128));
     TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
     auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src>;
+    // two or three tiles per workgroup: streamed side by side (one reduction)
+    if (src.per == 2) k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 2>;
+    if (src.per == 3) k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 3>;
     set_smem(k, smem);
     hipLaunchKernelGGL(k, dim3(grid), dim3(64 * NW), smem, s, (const uint4*)w->data, (const ST*)w->scales, x,
                        (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, EpiStore{y, (int)ldy}, NormArgs{}, src);
@@ -213,7 +214,11 @@ static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx
     const bool fits8 = Q4GemvSmem<8, 8>::bytes(GQ) <= 160 * 1024;    // staged rows fit LDS
     const bool fits16 = Q4GemvSmem<16, 16>::bytes(GQ) <= 160 * 1024;
     const bool fits4 = Q4GemvSmem<XF32 ? 8 : 4, 8>::bytes(GQ) <= 160 * 1024;
-    if (m <= 4 && fits4) q4_gemv_dispatch<XF32, ST>(w, x, m, ldx, y, ldy, s);
+    // m <= 2: one tile per workgroup; 3..16: a 4-, 8- or 16-row block staged
+    // once per workgroup over ceil(tiles / CUs) tiles (config 2, M=4: 8.3 ->
+    // 7.6 us; M=1 is faster with one tile per workgroup, 6.7 against 7.0)
+    if (m <= 2 && fits4) q4_gemv_dispatch<XF32, ST>(w, x, m, ldx, y, ldy, s);
+    else if (m <= 4 && fits4) q4_span_launch<4, XF32, ST>(w, x, m, ldx, y, ldy, s, cus);
     else if (XF32 && m <= 8 && fits16) q4_span_launch<8, true, ST>(w, x, m, ldx, y, ldy, s, cus);
     else if (!XF32 && m <= 8 && fits8) q4_span_launch<8, false, ST>(w, x, m, ldx, y, ldy, s, cus);
     else if (!XF32 && m <= 16 && fits16) q4_span_launch<16, false, ST>(w, x, m, ldx, y, ldy, s, cus);

@@ -343,8 +343,12 @@ struct EpiNoFinish {
 // gq = w + NW*i ("items"), stage only the activations they need in their own
 // LDS region (no workgroup barrier) and keep D items of weights in flight.
 // ---------------------------------------------------------------------------
+// PAR > 1 (multi-tile sources only): the workgroup's tiles (at most PAR)
+// are streamed side by side rather than one after another, every staged
+// activation fragment feeding PAR weight tiles, and one cross-wave
+// reduction at the end serves them all.
 template <int MR, bool XF32, bool VEC, typename ST, typename Epi, int D = 2, int WPE = 4, int NW = 4,
-          bool NORM = false, typename Src = SingleMatrix>
+          bool NORM = false, typename Src = SingleMatrix, int PAR = 1>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) void q4_gemv_kernel(
     const uint4* __restrict__ wt, const ST* __restrict__ sc, const void* __restrict__ xin, int K, int Kp, int N,
     int ldx, Epi epi, NormArgs norm, Src src = Src{}) {
@@ -440,10 +444,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     //    issued after its own.
     uint4 wbuf[D];
     typename SR::Rec sbuf[NS], scur;
+    static_assert(PAR == 1 || (Src::TPW > 1 && !NORM), "side-by-side tiles need a multi-tile source");
+    constexpr int PX = PAR > 1 ? PAR - 1 : 1;
+    uint4 wbx[PX][D];  // PAR > 1: items of tiles t+1 .. t+PAR-1
+    typename SR::Rec sbx[PX][NS];
+    // tile p of this workgroup (past its last tile: a duplicate of that tile, never stored)
+    auto tile_p = [&](int p) { return t + (p < ntl ? p : ntl - 1); };
 #pragma unroll
     for (int u = 0; u < D; u++) {
         if (u % SI == 0) sbuf[u / SI] = *scale_ptr(u);
         wbuf[u] = ldg_stream(wp + (size_t)item_gq(u) * 64);
+        if constexpr (PAR > 1) {
+#pragma unroll
+            for (int pp = 0; pp < PAR - 1; pp++) {
+                const int tp = tile_p(pp + 1);
+                if (u % SI == 0) sbx[pp][u / SI] = *scale_ptr_t(u, tp);
+                wbx[pp][u] = ldg_stream(wt + (size_t)tp * GQ * 64 + lane + (size_t)item_gq(u) * 64);
+            }
+        }
     }
     float inv_rms = 1.0f;
     if (NORM) {
@@ -621,6 +639,69 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         }
         if (trailing) lds_barrier();  // red and tilev are rewritten by the next tile
     };
+    if constexpr (PAR > 1) {
+        float accp[PAR][4];
+#pragma unroll
+        for (int pp = 0; pp < PAR; pp++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) accp[pp][e] = 0.0f;
+        typename SR::Rec scp[PAR];
+        auto stepP = [&](auto refill_tag, int u, int i) {
+#pragma unroll
+            for (int pp = 0; pp < PAR; pp++) {
+                const uint4 wv = pp == 0 ? wbuf[u] : wbx[pp - 1][u];
+                if (u % SI == 0) scp[pp] = pp == 0 ? sbuf[u / SI] : sbx[pp - 1][u / SI];
+                const typename SR::Rec sv = scp[pp];
+                if constexpr (decltype(refill_tag)::value) {
+                    const int tp = tile_p(pp);
+                    typename SR::Rec& sdst = pp == 0 ? sbuf[u / SI] : sbx[pp - 1][u / SI];
+                    uint4& wdst = pp == 0 ? wbuf[u] : wbx[pp - 1][u];
+                    if (u % SI == 0) sdst = *scale_ptr_t(i + D, tp);
+                    wdst = ldg_stream(wt + (size_t)tp * GQ * 64 + lane + (size_t)item_gq(i + D) * 64);
+                }
+                if (i >= nmine) continue;  // wave-uniform
+                float sj[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) sj[j] = SR::get(sv, u % SI, j);
+                item_mfma(i, wv, sj, accp[pp]);
+            }
+        };
+        const int nbatch = (nmine + D - 1) / D;
+        for (int bt = 0; bt + 1 < nbatch; bt++) {
+#pragma unroll
+            for (int u = 0; u < D; u++) stepP(std::true_type{}, u, bt * D + u);
+        }
+        if (nbatch > 0) {
+#pragma unroll
+            for (int u = 0; u < D; u++) stepP(std::false_type{}, u, (nbatch - 1) * D + u);
+        }
+        // One reduction for all PAR tiles: each wave's partials go to its
+        // own staging region (its activations are no longer read), then
+        // every output sums the waves in order, as tile_end does.
+        float* mine = (float*)wl;  // [PAR][RS][16]
+        if (q * 4 < MR) {
+#pragma unroll
+            for (int pp = 0; pp < PAR; pp++)
+#pragma unroll
+                for (int e = 0; e < ACC; e++)
+                    if (4 * q + e < MR) mine[(pp * RS + 4 * q + e) * 16 + r] = accp[pp][e];
+        }
+        lds_barrier();
+        for (int idx = tid; idx < PAR * 16 * M; idx += 64 * NW) {
+            const int pp = idx / (16 * M), m = (idx >> 4) % M, rr = idx & 15;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const float* rw = (const float*)((const char*)smem + (size_t)w * Q4GemvSmem<MR, NW>::per_wave(items_max)) +
+                                  pp * RS * 16;
+                if (XF32) v += rw[(2 * m) * 16 + rr] + rw[(2 * m + 1) * 16 + rr];
+                else v += rw[m * 16 + rr];
+            }
+            const int n = (t + pp) * 16 + rr;
+            if (pp < ntl && n < N && m < mrows) epi(src.out_row(m), n, v, nullptr, aux);
+        }
+        return;
+    }
     for (int tt = 0; tt < ntl; tt++) {  // one trip unless the source groups tiles
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         auto step = [&](auto refill_tag, int u, int i) {
