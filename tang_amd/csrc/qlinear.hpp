@@ -444,7 +444,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     //    issued after its own.
     uint4 wbuf[D];
     typename SR::Rec sbuf[NS], scur;
-    static_assert(PAR == 1 || (Src::TPW > 1 && !NORM), "side-by-side tiles need a multi-tile source");
+    static_assert(PAR == 1 || Src::TPW > 1, "side-by-side tiles need a multi-tile source");
     constexpr int PX = PAR > 1 ? PAR - 1 : 1;
     uint4 wbx[PX][D];  // PAR > 1: items of tiles t+1 .. t+PAR-1
     typename SR::Rec sbx[PX][NS];
@@ -687,6 +687,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
                     if (4 * q + e < MR) mine[(pp * RS + 4 * q + e) * 16 + r] = accp[pp][e];
         }
         lds_barrier();
+        // finished values of every tile: [PAR][M][16] in the (now unused)
+        // cross-wave reduction area
+        float* tv = red;
+        static_assert(PAR * 16 * M <= NW * RS * 16, "tile values fit the reduction area");
         for (int idx = tid; idx < PAR * 16 * M; idx += 64 * NW) {
             const int pp = idx / (16 * M), m = (idx >> 4) % M, rr = idx & 15;
             float v = 0.0f;
@@ -697,8 +701,24 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
                 if (XF32) v += rw[(2 * m) * 16 + rr] + rw[(2 * m + 1) * 16 + rr];
                 else v += rw[m * 16 + rr];
             }
-            const int n = (t + pp) * 16 + rr;
-            if (pp < ntl && n < N && m < mrows) epi(src.out_row(m), n, v, nullptr, aux);
+            tv[idx] = v;
+        }
+        lds_barrier();
+        // epilogues tile by tile (they may read their tile's values and run
+        // a per-tile finish hook)
+#pragma unroll
+        for (int pp = 0; pp < PAR; pp++) {
+            if (pp >= ntl) break;  // workgroup-uniform
+            if (tid < 16 * M) {
+                const int m = tid >> 4, rr = tid & 15;
+                const int n = (t + pp) * 16 + rr;
+                if (n < N && m < mrows) epi(src.out_row(m), n, tv[(pp * M + m) * 16 + rr], tv + (pp * M + m) * 16, aux);
+            }
+            if constexpr (Epi::HAS_FINISH) {
+                lds_barrier();
+                epi.finish(t + pp, (int)gridDim.x, aux, tid);
+                lds_barrier();  // aux is rewritten by the next tile's epilogue
+            }
         }
         return;
     }
