@@ -90,12 +90,13 @@ static void q4_span_launch_v(const th_qweight* w, const void* x, size_t m, size_
     src.per = (int)ceil_div((size_t)tiles, (size_t)cus);
     src.rows = (int)m;
     const unsigned grid = (unsigned)ceil_div((size_t)tiles, (size_t)src.per);
-    const size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w->Kp / 128));
-    TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
+    size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w->Kp / 128));
     auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src>;
     // two or three tiles per workgroup: streamed side by side (one reduction)
     if (src.per == 2) k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 2>;
     if (src.per == 3) k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 3>;
+    if (src.per == 2 || src.per == 3) smem += Q4GemvSmem<MR, NW>::par_bytes(src.per);
+    TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
     set_smem(k, smem);
     hipLaunchKernelGGL(k, dim3(grid), dim3(64 * NW), smem, s, (const uint4*)w->data, (const ST*)w->scales, x,
                        (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, EpiStore{y, (int)ldy}, NormArgs{}, src);

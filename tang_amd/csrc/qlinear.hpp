@@ -227,6 +227,8 @@ struct Q4GemvSmem {
         const int items = (GQ + NW - 1) / NW;
         return NW * per_wave(items) + NW * RS * 16 * 4 + 16 * 16 * 4 + 16 * 4;
     }
+    // extra bytes of a launch whose tiles are streamed side by side (PAR)
+    static constexpr size_t par_bytes(int par) { return par > 1 ? (size_t)par * 16 * (MR <= 8 ? 8 : 16) * 4 : 0; }
 };
 
 // Default source of a GEMV workgroup: one weight matrix, tile = blockIdx.x,
@@ -687,10 +689,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
                     if (4 * q + e < MR) mine[(pp * RS + 4 * q + e) * 16 + r] = accp[pp][e];
         }
         lds_barrier();
-        // finished values of every tile: [PAR][M][16] in the (now unused)
-        // cross-wave reduction area
-        float* tv = red;
-        static_assert(PAR * 16 * M <= NW * RS * 16, "tile values fit the reduction area");
+        // finished values of every tile: [PAR][M][16] after the epilogue
+        // scratch (the launch adds Q4GemvSmem::par_bytes)
+        float* tv = aux + 16;
         for (int idx = tid; idx < PAR * 16 * M; idx += 64 * NW) {
             const int pp = idx / (16 * M), m = (idx >> 4) % M, rr = idx & 15;
             float v = 0.0f;
