@@ -263,12 +263,16 @@ void launch_q4_linear(const th_qweight* w, const void* x, th_dtype xdt, size_t m
 
 template <int M, bool XF32, bool PR, bool VEC>
 static void q8_launch_v(const th_qweight* w, const void* x, size_t ldx, float* y, size_t ldy, hipStream_t s) {
-    const size_t smem = Q8GemvSmem<M>::bytes((int)w->Kp);
+    // eight waves split each tile's K (config 1: 5.33 us; four waves 5.88,
+    // sixteen 6.2-6.3; 2, 6 or 8 chunks in flight per wave instead of 4 were
+    // slower)
+    constexpr int NW = 8;
+    const size_t smem = Q8GemvSmem<M, NW>::bytes((int)w->Kp);
     TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
-    auto k = q8_gemv_kernel<M, XF32, VEC, PR, EpiStore>;
+    auto k = q8_gemv_kernel<M, XF32, VEC, PR, EpiStore, NW>;
     set_smem(k, smem);
     EpiStore epi{y, (int)ldy};
-    hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(256), smem, s, (const uint4*)w->data,
+    hipLaunchKernelGGL(k, dim3((unsigned)(w->Np / 16)), dim3(64 * NW), smem, s, (const uint4*)w->data,
                        (const float*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)ldx, epi);
     TH_LAUNCH_CHECK();
 }

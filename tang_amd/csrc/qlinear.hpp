@@ -768,23 +768,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 }
 
 // ---------------------------------------------------------------------------
-// int8 GEMV, VALU path.  One workgroup = one 16-row tile; waves take chunks
-// c = wave, wave+4, ...  x is staged in LDS as f32 with
+// int8 GEMV, VALU path.  One workgroup = one 16-row tile; its NW waves take
+// chunks c = wave, wave+NW, ...  x is staged in LDS as f32 with
 // bias[m][c][q] = -128 * sum of the 16 x values of lane-quad q, so that
 // sum((q8 ^ 0x80) * x) + bias = sum(q8 * x).
 // ---------------------------------------------------------------------------
 
-template <int M>
+template <int M, int NW = 4>
 struct Q8GemvSmem {
-    static size_t bytes(int Kp) { return (size_t)M * Kp * 4 + (size_t)M * (Kp / 16) * 4 + 5 * 16 * M * 4 + 64 * 4; }
+    static size_t bytes(int Kp) { return (size_t)M * Kp * 4 + (size_t)M * (Kp / 16) * 4 + (NW + 1) * 16 * M * 4 + 64 * 4; }
 };
 
-template <int M, bool XF32, bool VEC, bool PER_ROW, typename Epi>
-__global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ wt,
+template <int M, bool XF32, bool VEC, bool PER_ROW, typename Epi, int NW = 4, int DQ = 4>
+__global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(const uint4* __restrict__ wt,
                                                       const float* __restrict__ sc,
                                                       const void* __restrict__ xin, int K, int Kp,
                                                       int N, int ldx, Epi epi) {
-    constexpr int D = 4;  // weight chunks in flight per wave (2: 7.5 us, 4: 5.8, 6: 6.0, 8: 5.9, 16: 7.3 on config 1)
+    constexpr int D = DQ;  // weight chunks in flight per wave (4: best on config 1 with 4 or 8 waves)
     constexpr int XB = 4;  // 16-element x chunks per thread loaded ahead of the weights
     extern __shared__ uint4 smem[];
     const int NCH = Kp >> 6;  // 64-element chunks
@@ -796,17 +796,17 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
     const int t = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int q = lane >> 4, r = lane & 15;
-    const int nmine = (NCH - wave + 3) >> 2;
+    const int nmine = (NCH - wave + NW - 1) / NW;
     const uint4* wp = wt + (size_t)t * NCH * 64 + lane;
     const int row = t * 16 + r;
     const int GPR = Kp >> 5;  // groups per row (per-group scales)
     const int nchunks = M * N16;
-    auto item_off = [&](int i) { return (size_t)(i < nmine ? wave + 4 * i : 0) * 64; };
+    auto item_off = [&](int i) { return (size_t)(i < nmine ? wave + NW * i : 0) * 64; };
 
     uint4 xa[XB][2], xb[XB][2];
 #pragma unroll
     for (int b = 0; b < XB; b++) {
-        int c = tid + b * 256;
+        int c = tid + b * 64 * NW;
         c = c < nchunks ? c : nchunks - 1;
         const int m = c / N16, k0 = (c - m * N16) * 16;
         load_x8<XF32, VEC>(xin, m, ldx, K, k0, xa[b][0], xb[b][0]);
@@ -845,10 +845,10 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
     };
 #pragma unroll
     for (int b = 0; b < XB; b++) {
-        const int c = tid + b * 256;
+        const int c = tid + b * 64 * NW;
         if (c < nchunks) stage(c, xa[b], xb[b]);
     }
-    for (int c = tid + XB * 256; c < nchunks; c += 256) {
+    for (int c = tid + XB * 64 * NW; c < nchunks; c += 64 * NW) {
         uint4 a[2], b2[2];
         const int m = c / N16, k0 = (c - m * N16) * 16;
         load_x8<XF32, VEC>(xin, m, ldx, K, k0, a[0], b2[0]);
@@ -863,7 +863,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
 
     auto step = [&](auto refill_tag, int u, int i) {
         const bool valid = i < nmine;
-        const int c = valid ? wave + 4 * i : 0;
+        const int c = valid ? wave + NW * i : 0;
         const uint32_t wv[4] = {wbuf[u].x ^ 0x80808080u, wbuf[u].y ^ 0x80808080u,
                                 wbuf[u].z ^ 0x80808080u, wbuf[u].w ^ 0x80808080u};
         if constexpr (decltype(refill_tag)::value) wbuf[u] = ldg_stream(wp + item_off(i + D));
@@ -902,13 +902,13 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(const uint4* __restrict__ 
         if (q == 0) red[(wave * M + m) * 16 + r] = v;
     }
     __syncthreads();
-    float* tilev = red + 4 * 16 * M;  // [M][16]
+    float* tilev = red + NW * 16 * M;  // [M][16]
     float v = 0.0f;
     if (tid < 16 * M) {
         const int m = tid >> 4, rr = tid & 15;
         v = red[(0 * M + m) * 16 + rr] + red[(1 * M + m) * 16 + rr];
-        v += red[(2 * M + m) * 16 + rr];
-        v += red[(3 * M + m) * 16 + rr];
+#pragma unroll
+        for (int w = 2; w < NW; w++) v += red[(w * M + m) * 16 + rr];
         const int n = t * 16 + rr;
         if (PER_ROW) v *= sc[n < N ? n : 0];
         tilev[m * 16 + rr] = v;
