@@ -94,6 +94,35 @@ def prefill_bench(dev, m, steps=30):
     return dict(M=m, us=round(us, 1), tflops=round(tf, 1), frac_mfma_bf16=round(tf / PEAK_BF16_TFLOPS, 4))
 
 
+def blas_reference():
+    """The library's plain dense GEMM (torch.matmul on ROCm: hipBLASLt) on the
+    prefill GEMM shapes, as a reference point for the MFMA rate this part
+    sustains on random and on constant operands.  Not part of the bench line."""
+    import torch
+    out = []
+    dev = torch.device("cuda:0")
+    for dt, name in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+        for m in (512, 2048):
+            for fill in ("randn", "ones"):
+                if fill == "ones" and (dt != torch.float16 or m != 2048):
+                    continue
+                mk = torch.randn if fill == "randn" else torch.ones
+                a, b = mk(m, K, dtype=dt, device=dev), mk(N, K, dtype=dt, device=dev)
+                for _ in range(5):
+                    a @ b.t()
+                torch.cuda.synchronize()
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                for _ in range(50):
+                    a @ b.t()
+                e.record()
+                torch.cuda.synchronize()
+                us = s.elapsed_time(e) * 1e3 / 50
+                out.append(dict(dtype=name, M=m, operands=fill, us=round(us, 1),
+                                tflops=round(2.0 * m * N * K / us / 1e6, 1)))
+    return {"blas_reference": out, "shape": "M x 4096 times (11008 x 4096)^T"}
+
+
 def decode_bytes_per_token(c, t_attended):
     """Algorithmic HBM bytes of one decode step: every weight byte, the KV
     rows attended, norms and one embedding row, each counted once."""
@@ -356,12 +385,18 @@ def main():
                     help="counter runs: 240 stream-launched config-2 GEMVs at this batch size")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="counter runs: four M=2048 prefill GEMMs on the config-2 matrix")
+    ap.add_argument("--blas-ref", action="store_true",
+                    help="reference point only: the library's dense f16/bf16 GEMM (torch.matmul) on the prefill "
+                         "shapes, random and all-ones operands")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (collectives are out of scope); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.blas_ref:
+        print(json.dumps(blas_reference()))
+        return
     dev = capi.HipComputeDevice(0)
     if args.profile_m:
         gemv_bench(dev, args.profile_m, 240, 0, graph=False)
