@@ -409,7 +409,7 @@ static void gemv_engine(const th_qweight* w, const void* x, NormArgs norm, Epi e
                            (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm, SingleMatrix{});
     } else if (NORM && w->Np / 16 >= 1376) {  // many tiles (gate/up, LM head): two per workgroup, one staging
         // (QKV's 768 tiles run faster one per workgroup: 709 against 723 tok/s)
-        const size_t smem = Q4GemvSmem<1, 4>::bytes((int)(w->Kp / 128)) + Q4GemvSmem<1, 4>::par_bytes(2);
+        const size_t smem = Q4GemvSmem<1, 4, 2>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
         SingleMatrixTiles<2> src;
         src.tiles = (int)(w->Np / 16);

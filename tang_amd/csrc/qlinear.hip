@@ -90,12 +90,17 @@ static void q4_span_launch_v(const th_qweight* w, const void* x, size_t m, size_
     src.per = (int)ceil_div((size_t)tiles, (size_t)cus);
     src.rows = (int)m;
     const unsigned grid = (unsigned)ceil_div((size_t)tiles, (size_t)src.per);
-    size_t smem = Q4GemvSmem<MR, NW>::bytes((int)(w->Kp / 128));
+    const int GQ = (int)(w->Kp / 128);
+    size_t smem = Q4GemvSmem<MR, NW>::bytes(GQ);
     auto k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src>;
     // two or three tiles per workgroup: streamed side by side (one reduction)
-    if (src.per == 2) k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 2>;
-    if (src.per == 3) k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 3>;
-    if (src.per == 2 || src.per == 3) smem += Q4GemvSmem<MR, NW>::par_bytes(src.per);
+    if (src.per == 2) {
+        k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 2>;
+        smem = Q4GemvSmem<MR, NW, 2>::bytes(GQ);
+    } else if (src.per == 3) {
+        k = q4_gemv_kernel<MR, XF32, VEC, ST, EpiStore, 2, WPE, NW, false, Src, 3>;
+        smem = Q4GemvSmem<MR, NW, 3>::bytes(GQ);
+    }
     TH_REQUIRE(smem <= 160 * 1024, "activation too large for the LDS-staged GEMV");
     set_smem(k, smem);
     hipLaunchKernelGGL(k, dim3(grid), dim3(64 * NW), smem, s, (const uint4*)w->data, (const ST*)w->scales, x,
@@ -212,9 +217,10 @@ template <bool XF32, typename ST>
 static void q4_linear_t(const th_qweight* w, const void* x, size_t m, size_t ldx, float* y, size_t ldy,
                         hipStream_t s, th_device* dev, void* ws = nullptr, size_t ws_bytes = 0) {
     const int GQ = (int)(w->Kp / 128), cus = dev && dev->num_cus > 0 ? dev->num_cus : 256;
-    const bool fits8 = Q4GemvSmem<8, 8>::bytes(GQ) <= 160 * 1024;    // staged rows fit LDS
-    const bool fits16 = Q4GemvSmem<16, 16>::bytes(GQ) <= 160 * 1024;
-    const bool fits4 = Q4GemvSmem<XF32 ? 8 : 4, 8>::bytes(GQ) <= 160 * 1024;
+    // staged rows fit LDS (with the side-by-side tiles' extra, the largest case)
+    const bool fits8 = Q4GemvSmem<8, 8, 3>::bytes(GQ) <= 160 * 1024;
+    const bool fits16 = Q4GemvSmem<16, 16, 3>::bytes(GQ) <= 160 * 1024;
+    const bool fits4 = Q4GemvSmem<XF32 ? 8 : 4, 8, 3>::bytes(GQ) <= 160 * 1024;
     // m <= 2: one tile per workgroup; 3..16: a 4-, 8- or 16-row block staged
     // once per workgroup over ceil(tiles / CUs) tiles (config 2, M=4: 8.3 ->
     // 7.6 us; M=1 is faster with one tile per workgroup, 6.7 against 7.0)

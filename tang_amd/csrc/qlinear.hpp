@@ -217,18 +217,24 @@ inline size_t q4_scale_count(bool f16, size_t NT, size_t GQ) {
 // LDS bytes of the MFMA GEMV: per wave, x as [item][j][MR][q] 16-byte
 // chunks plus a zero chunk and the bias as [item][j][8] floats; then the
 // cross-wave reduction [NW][8][16], the finished tile [M][16] and 16 floats
-// of epilogue scratch.
-template <int MR, int NW = 4>
+// of epilogue scratch.  PAR > 1 (tiles streamed side by side): each wave's
+// region also holds its partials of the PAR tiles once its items are done
+// ([PAR][RS][16] floats, so the region is at least that large), and the
+// finished values of all PAR tiles ([PAR][M][16]) follow the scratch.
+template <int MR, int NW = 4, int PAR = 1>
 struct Q4GemvSmem {
     static constexpr int BS = MR <= 8 ? 8 : 16;  // bias floats per (item, group)
     static constexpr int RS = MR <= 8 ? 8 : 16;  // reduction rows
-    __host__ __device__ static size_t per_wave(int items) { return (size_t)items * 4 * (MR * 64 + BS * 4) + 16; }
+    __host__ __device__ static size_t per_wave(int items) {
+        const size_t staging = (size_t)items * 4 * (MR * 64 + BS * 4) + 16;
+        const size_t partials = PAR > 1 ? (size_t)PAR * RS * 16 * 4 : 0;
+        return staging > partials ? staging : partials;
+    }
     static size_t bytes(int GQ) {
         const int items = (GQ + NW - 1) / NW;
-        return NW * per_wave(items) + NW * RS * 16 * 4 + 16 * 16 * 4 + 16 * 4;
+        const size_t tiles = PAR > 1 ? (size_t)PAR * 16 * RS * 4 : 0;
+        return NW * per_wave(items) + NW * RS * 16 * 4 + 16 * 16 * 4 + 16 * 4 + tiles;
     }
-    // extra bytes of a launch whose tiles are streamed side by side (PAR)
-    static constexpr size_t par_bytes(int par) { return par > 1 ? (size_t)par * 16 * (MR <= 8 ? 8 : 16) * 4 : 0; }
 };
 
 // Default source of a GEMV workgroup: one weight matrix, tile = blockIdx.x,
@@ -362,7 +368,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     constexpr bool LOADF32 = XF32 || NORM;
     static_assert(!NORM || (MR == 1 && !XF32), "the RMSNorm prologue serves one bf16 row");
     static_assert(D % SI == 0, "prefetch depth must cover whole scale records");
-    constexpr int BS = Q4GemvSmem<MR, NW>::BS, RS = Q4GemvSmem<MR, NW>::RS;
+    using Smem = Q4GemvSmem<MR, NW, PAR>;
+    constexpr int BS = Smem::BS, RS = Smem::RS;
     extern __shared__ uint4 smem[];
     const int GQ = Kp >> 7;
     const int items_max = (GQ + NW - 1) / NW;
@@ -382,11 +389,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     const int nmine = (GQ - wave + NW - 1) / NW;  // items of this wave (wave-uniform)
 
     // per-wave LDS region
-    char* wl = (char*)smem + (size_t)wave * Q4GemvSmem<MR, NW>::per_wave(items_max);
+    char* wl = (char*)smem + (size_t)wave * Smem::per_wave(items_max);
     uint4* xw = (uint4*)wl;                                   // [item][j][MR][4]
     uint4* zero = xw + (size_t)items_max * 4 * MR * 4;        // one zero chunk
     float* bw = (float*)(zero + 1);                           // [item][j][BS]
-    float* red = (float*)((char*)smem + NW * Q4GemvSmem<MR, NW>::per_wave(items_max));  // [NW][RS][16]
+    float* red = (float*)((char*)smem + NW * Smem::per_wave(items_max));  // [NW][RS][16]
     float* tilev = red + NW * RS * 16;                        // [M][16]
     float* aux = tilev + 16 * 16;                             // [16]
 
@@ -689,15 +696,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
                     if (4 * q + e < MR) mine[(pp * RS + 4 * q + e) * 16 + r] = accp[pp][e];
         }
         lds_barrier();
-        // finished values of every tile: [PAR][M][16] after the epilogue
-        // scratch (the launch adds Q4GemvSmem::par_bytes)
+        // finished values of every tile: [PAR][M][16] after the epilogue scratch
         float* tv = aux + 16;
         for (int idx = tid; idx < PAR * 16 * M; idx += 64 * NW) {
             const int pp = idx / (16 * M), m = (idx >> 4) % M, rr = idx & 15;
             float v = 0.0f;
 #pragma unroll
             for (int w = 0; w < NW; w++) {
-                const float* rw = (const float*)((const char*)smem + (size_t)w * Q4GemvSmem<MR, NW>::per_wave(items_max)) +
+                const float* rw = (const float*)((const char*)smem + (size_t)w * Smem::per_wave(items_max)) +
                                   pp * RS * 16;
                 if (XF32) v += rw[(2 * m) * 16 + rr] + rw[(2 * m + 1) * 16 + rr];
                 else v += rw[m * 16 + rr];

@@ -37,6 +37,25 @@ def test_small_llama_matches_oracle(dev):
     assert max_abs_rel(logits, r_logits) < 1e-3
 
 
+def test_narrow_model_wide_ffn_matches_oracle(dev):
+    """d_model 256 with an 11008-wide FFN and a 22016-row LM head: the
+    gate/up and LM-head GEMVs take two tiles per workgroup side by side on
+    a K short enough that a wave holds a single 128-wide item."""
+    cfg = dict(CONFIG_SMALL, n_layers=1, d_ff=11008, vocab=22016)
+    seed, kv_seed, prefill, steps = 5, 6, 40, 12
+    ref = OracleLlama(cfg, seed, kv_seed, prefill)
+    r_toks, margins, r_logits = ref.generate(1, prefill, steps)
+    m = device_llama(dev, cfg, seed, kv_seed, prefill)
+    try:
+        toks, logits = device_generate(m, cfg, 1, prefill, steps)
+    finally:
+        capi.lib().th_llama_destroy(m)
+    print("oracle", r_toks, "min margin %.3e" % min(margins))
+    print("device", list(toks))
+    assert list(toks) == r_toks
+    assert max_abs_rel(logits, r_logits) < 1e-3
+
+
 def test_small_llama_long_context_matches_oracle(dev):
     """Positions past 4096: more than sixteen 256-position attention splits,
     so the last split's merge takes a second round of records."""

@@ -97,6 +97,32 @@ def test_q4_config2_batched(dev, rows, cols, m):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("rows", [9600, 6000])  # 600 / 375 tiles: three / two per workgroup, side by side
+@pytest.mark.parametrize("cols", [130, 256, 1000])  # one to eight 128-wide items: a wave may hold one item
+@pytest.mark.parametrize("m,dt", [(3, "bf16"), (4, "bf16"), (8, "bf16"), (16, "bf16"), (2, "f32"), (4, "f32"),
+                                  (7, "f32")])
+def test_q4_gemv_side_by_side_tiles_short_k(dev, rows, cols, m, dt):
+    """Workgroups streaming two or three tiles side by side, on short K,
+    where a wave's staging region is smaller than its partials of all the
+    tiles (the region is sized for both)."""
+    print(f"q4 side-by-side rows={rows} cols={cols} m={m} {dt}", flush=True)
+    nib, sc16, sc = _q4_case(rows, cols, 31 + m)
+    w = dev.q4_upload_packed(nib, sc16, rows, cols, capi.F16)
+    if dt == "bf16":
+        xb = capi.synth_normal(40 + m, m * cols, 1.0, capi.BF16)
+        y = dev.gemm_q4(dev.upload(xb, capi.BF16), m, w).to_numpy().reshape(m, rows)
+        ref = _ref_q4(nib, sc, rows, cols, oracle.bf16_to_f32(xb).reshape(m, cols).astype(np.float64))
+        tol = TOL_BF16
+    else:
+        xf = capi.synth_normal(40 + m, m * cols, 1.0, capi.F32)
+        y = dev.gemm_q4(dev.upload(xf), m, w).to_numpy().reshape(m, rows)
+        ref = _ref_q4(nib, sc, rows, cols, xf.reshape(m, cols).astype(np.float64))
+        tol = TOL_F32
+    err = max_abs_rel(y, ref)
+    print("max_abs_rel", err)
+    assert err < tol
+
+
 def test_q4_reference_blocks_f32_scales(dev):
     """Weights produced by the reference quantizer (f32 scales, ragged K)."""
     rng = np.random.default_rng(0)
