@@ -19,6 +19,7 @@
 // Grouped launches size the grid for the worst case; work items past the
 // real ones return at once.
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "capi_util.hpp"
@@ -114,10 +115,13 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
 // index.  Every lane counts its experts' ranks against the probabilities in
 // the wave's LDS row sp[E] (no serial reductions); the expert of rank r < k
 // writes entry r of the token to idx[r], w[r].
+// PL: expert slots per lane, ceil(E / 64) (a compile-time count, so a
+// 64-expert router runs one slot without per-slot guards)
+template <int PL>
 __device__ __forceinline__ void moe_topk_token(const float* __restrict__ logits, int t, int E, int k, int32_t* idx,
                                                float* w, float* sp) {
     const int lane = threadIdx.x & 63;
-    constexpr int PL = MOE_MAX_E / 64;
+    static_assert(PL >= 1 && PL * 64 <= MOE_MAX_E, "slots per lane");
     float p[PL];
     float mx = -INFINITY;
 #pragma unroll
@@ -135,17 +139,34 @@ __device__ __forceinline__ void moe_topk_token(const float* __restrict__ logits,
     }
     sum = group_sum<64>(sum);
     const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < PL; i++) p[i] = p[i] * inv;
+    if constexpr (PL == 1) {
+        // One expert per lane: k rounds of a wave argmax (DPP maximum, then
+        // the lowest lane holding it), the same order as the ranks below at
+        // a fifth of the instructions (the rank count compares every lane
+        // with all 64 experts).
+        float v = lane < E ? p[0] : -INFINITY;
+        for (int r = 0; r < k; r++) {  // k <= E
+            const float m = group_max<64>(v);
+            const int win = (int)__builtin_ctzll(__ballot(v == m));
+            if (lane == 0) {
+                idx[r] = win;
+                w[r] = m;
+            }
+            if (lane == win) v = -INFINITY;
+        }
+        return;
+    }
     const int E16 = (E + 15) & ~15;  // sp is padded to whole 16-float rounds with -inf
 #pragma unroll
     for (int i = 0; i < PL; i++) {
-        p[i] = p[i] * inv;
         const int e = lane + 64 * i;
         if (e < E16) sp[e] = e < E ? p[i] : -INFINITY;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-    const int pl = (E + 63) >> 6;  // lane slots holding experts
     int rank[PL];
 #pragma unroll
     for (int i = 0; i < PL; i++) rank[i] = 0;
@@ -157,13 +178,11 @@ __device__ __forceinline__ void moe_topk_token(const float* __restrict__ logits,
             pj[4 * u] = v.x; pj[4 * u + 1] = v.y; pj[4 * u + 2] = v.z; pj[4 * u + 3] = v.w;
         }
 #pragma unroll
-        for (int i = 0; i < PL; i++)
-            if (i < pl) {
-                const int e = lane + 64 * i;
+        for (int i = 0; i < PL; i++) {
+            const int e = lane + 64 * i;
 #pragma unroll
-                for (int u = 0; u < 16; u++)
-                    rank[i] += (pj[u] > p[i] || (pj[u] == p[i] && j0 + u < e)) ? 1 : 0;
-            }
+            for (int u = 0; u < 16; u++) rank[i] += (pj[u] > p[i] || (pj[u] == p[i] && j0 + u < e)) ? 1 : 0;
+        }
     }
 #pragma unroll
     for (int i = 0; i < PL; i++)
@@ -173,12 +192,13 @@ __device__ __forceinline__ void moe_topk_token(const float* __restrict__ logits,
         }
 }
 
+template <int PL>
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                        int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
     __shared__ __align__(16) float sp[4][MOE_MAX_E];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
-    moe_topk_token(logits, t, E, k, topk_idx + (size_t)t * k, topk_w + (size_t)t * k, sp[threadIdx.x >> 6]);
+    moe_topk_token<PL>(logits, t, E, k, topk_idx + (size_t)t * k, topk_w + (size_t)t * k, sp[threadIdx.x >> 6]);
 }
 
 // Slot assignment, deterministic: slots are grouped by expert (routed
@@ -193,6 +213,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
 // and keeps the indices in LDS for the slot passes: one launch instead of two
 // for decode-sized batches.
 constexpr int MOE_FUSED_ENTRIES = 1024;
+template <int PL>
 __global__ __launch_bounds__(1024) void moe_dispatch_kernel(const float* __restrict__ logits, int32_t* __restrict__ topk_idx_out,
                                                             float* __restrict__ topk_w_out,
                                                             const int32_t* __restrict__ topk_idx_in, int T, int k, int E,
@@ -208,7 +229,7 @@ __global__ __launch_bounds__(1024) void moe_dispatch_kernel(const float* __restr
     if (logits) {
         // the wave's row of cnt (zeroed below) holds its probabilities
         for (int t = wave; t < T; t += 16)
-            moe_topk_token(logits, t, E, k, sidx + t * k, sw + t * k, (float*)cnt[wave]);
+            moe_topk_token<PL>(logits, t, E, k, sidx + t * k, sw + t * k, (float*)cnt[wave]);
         __syncthreads();
         for (int i = tid; i < T * k; i += 1024) {
             topk_idx_out[i] = sidx[i];
@@ -661,15 +682,24 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
                        dim3(256), 0, s, (const uint16_t*)h->ptr, m->router, (int)T, (int)m->E, (int)m->d, m->logits);
     TH_LAUNCH_CHECK();
     const bool fused = T * m->k <= (size_t)MOE_FUSED_ENTRIES && T <= (size_t)MOE_SMALL_T;  // top-k inside dispatch
-    if (!fused) {
-        hipLaunchKernelGGL(moe_topk_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, s, m->logits, (int)T,
-                           (int)m->E, (int)m->k, (int32_t*)topk_idx->ptr, (float*)topk_w->ptr);
+    auto route = [&](auto pl_tag) {  // top-k and dispatch with ceil(E / 64) expert slots per lane
+        constexpr int PL = decltype(pl_tag)::value;
+        if (!fused) {
+            hipLaunchKernelGGL(moe_topk_kernel<PL>, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, s, m->logits, (int)T,
+                               (int)m->E, (int)m->k, (int32_t*)topk_idx->ptr, (float*)topk_w->ptr);
+            TH_LAUNCH_CHECK();
+        }
+        hipLaunchKernelGGL(moe_dispatch_kernel<PL>, dim3(1), dim3(1024), 0, s, fused ? (const float*)m->logits : nullptr,
+                           (int32_t*)topk_idx->ptr, (float*)topk_w->ptr, (const int32_t*)topk_idx->ptr, (int)T, (int)m->k,
+                           (int)m->E, (int)m->S, rows, m->offsets, m->slot_token, m->token_slot, m->work, (int)max_work);
         TH_LAUNCH_CHECK();
+    };
+    switch ((m->E + 63) / 64) {
+        case 1: route(std::integral_constant<int, 1>{}); break;
+        case 2: route(std::integral_constant<int, 2>{}); break;
+        case 3: route(std::integral_constant<int, 3>{}); break;
+        default: route(std::integral_constant<int, 4>{}); break;
     }
-    hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(1024), 0, s, fused ? (const float*)m->logits : nullptr,
-                       (int32_t*)topk_idx->ptr, (float*)topk_w->ptr, (const int32_t*)topk_idx->ptr, (int)T, (int)m->k,
-                       (int)m->E, (int)m->S, rows, m->offsets, m->slot_token, m->token_slot, m->work, (int)max_work);
-    TH_LAUNCH_CHECK();
     const uint16_t* hx = (const uint16_t*)h->ptr;
     if (rows == MOE_MIN_ROWS) {
         moe_grouped_gemv<MOE_MIN_ROWS, EpiMoeSwiGLU, 4>(m, m->gu[0], m->gu_data, m->gu_scales, hx, m->slot_token,
