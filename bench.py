@@ -188,7 +188,9 @@ MLA = dict(B=8, H=16, L=4096, dn=128, dr=64, r=512, dv=128)
 def moe_bench(dev, T, iters):
     """Config 4 MoE layer forward (router, dispatch, grouped int4 experts,
     combine) on T tokens.  Algorithmic bytes: every weight byte of the experts
-    the batch routes to (+ shared experts) once, the router, h in, out."""
+    the batch routes to (+ shared experts) once, the router, h in, out.
+    `us`: the calls replayed as one HIP graph (the decode loop's launch
+    mode); `stream_launched_us`: the same calls enqueued one by one."""
     import ctypes
     c = MOE
     L = capi.lib()
@@ -198,13 +200,20 @@ def moe_bench(dev, T, iters):
         capi.check(L.th_moe_init_synthetic(h, 4))
         x = dev.upload(capi.synth_normal(45, T * c["d"], 1.0, capi.BF16), capi.BF16)
         out, idx, w = dev.alloc(T * c["d"]), dev.alloc(T * c["k"], capi.I32), dev.alloc(T * c["k"])
+        fwd = lambda: capi.check(L.th_moe_forward(h, x.handle, T, out.handle, idx.handle, w.handle))
         for _ in range(5):
-            capi.check(L.th_moe_forward(h, x.handle, T, out.handle, idx.handle, w.handle))
+            fwd()
         dev.sync()
         dev.timer_start()
         for _ in range(iters):
-            capi.check(L.th_moe_forward(h, x.handle, T, out.handle, idx.handle, w.handle))
+            fwd()
+        ms_stream = dev.timer_stop()
+        g = dev.capture(lambda: [fwd() for _ in range(iters)])
+        g.launch()
+        dev.timer_start()
+        g.launch()
         ms = dev.timer_stop()
+        g.free()
         used = len(np.unique(idx.to_numpy())) + c["S"]
     finally:
         L.th_moe_destroy(h)
@@ -213,13 +222,15 @@ def moe_bench(dev, T, iters):
     us = ms * 1e3 / iters
     flops = 2 * T * (c["k"] + c["S"]) * lin
     return dict(T=T, us=round(us, 2), experts_read=used, bytes=int(nbytes), gbs=round(nbytes / us / 1e3, 1),
-                frac_hbm=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), tflops=round(flops / us / 1e6, 2))
+                frac_hbm=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), tflops=round(flops / us / 1e6, 2),
+                stream_launched_us=round(ms_stream * 1e3 / iters, 2))
 
 
 def mla_bench(dev, iters, copies=8):
     """Config 5 absorbed MLA decode, B=8 sequences x 4096 latent positions.
     Rotates `copies` caches (8 x 37.7 MB > 256 MB MALL).  Algorithmic bytes:
-    the latent cache, W_UK and W_UV with their scales, q in, out."""
+    the latent cache, W_UK and W_UV with their scales, q in, out.  `us`: the
+    calls replayed as one HIP graph; `stream_launched_us`: enqueued one by one."""
     c = MLA
     B, H, Lk, dn, dr, r, dv = c["B"], c["H"], c["L"], c["dn"], c["dr"], c["r"], c["dv"]
     qn = dev.upload(capi.synth_normal(1, B * H * dn, 1.0, capi.F32))
@@ -233,16 +244,23 @@ def mla_bench(dev, iters, copies=8):
     for i in range(copies):
         dev.mla_decode(qn, qr, caches[i], B, H, Lk, dn, dr, r, dv, wuk, wuv, scale, out)
     dev.sync()
+    call = lambda i: dev.mla_decode(qn, qr, caches[i % copies], B, H, Lk, dn, dr, r, dv, wuk, wuv, scale, out)
     dev.timer_start()
     for i in range(iters):
-        dev.mla_decode(qn, qr, caches[i % copies], B, H, Lk, dn, dr, r, dv, wuk, wuv, scale, out)
+        call(i)
+    ms_stream = dev.timer_stop()
+    g = dev.capture(lambda: [call(i) for i in range(iters)])
+    g.launch()
+    dev.timer_start()
+    g.launch()
     ms = dev.timer_stop()
+    g.free()
     us = ms * 1e3 / iters
     nbytes = B * Lk * (r + dr) * 2 + H * r * (dn + 4) + H * dv * (r + 4) + B * H * (dn + dr + dv) * 4
     for b in caches:
         b.free()
     return dict(us=round(us, 2), bytes=int(nbytes), gbs=round(nbytes / us / 1e3, 1),
-                frac_hbm=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4))
+                frac_hbm=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), stream_launched_us=round(ms_stream * 1e3 / iters, 2))
 
 
 def cpu_baseline(budget_s=12.0, threads=1):

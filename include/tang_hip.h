@@ -47,6 +47,7 @@ typedef enum {
 typedef struct th_device th_device;
 typedef struct th_buffer th_buffer;
 typedef struct th_qweight th_qweight;
+typedef struct th_graph th_graph;
 
 /* Reference block layouts (crates/tang-infer/src/quantize.rs:15-29), as plain
  * C structs: Q8Block {scale; values[32]} and Q4Block {scale; values[16]} with
@@ -71,6 +72,17 @@ int th_memory_info(th_device* dev, size_t* free_bytes, size_t* total_bytes);
  * events; stop synchronises and returns elapsed milliseconds. */
 int th_timer_start(th_device* dev);
 int th_timer_stop(th_device* dev, float* ms);
+/* Record the library calls made on the device stream between begin and end
+ * into one HIP graph, replayed by th_graph_launch on the same stream.  No
+ * counterpart in the reference (its backends launch every call): this is
+ * for callers that repeat a fixed sequence of calls, as a decode loop does.
+ * The recorded calls must not allocate: make each one once before capture
+ * (workspaces grow on first use).  Replays read and write the same buffers
+ * the recorded calls named. */
+int th_capture_begin(th_device* dev);
+int th_capture_end(th_device* dev, th_graph** out);
+int th_graph_launch(th_graph* g);
+int th_graph_destroy(th_graph* g);
 
 /* ---- buffers (device.rs:44-80 upload/upload_u32/alloc/download) -------- */
 

@@ -52,6 +52,10 @@ SIGNATURES = {
     "th_memory_info": ([_P, _P, _P], _I),
     "th_timer_start": ([_P], _I),
     "th_timer_stop": ([_P, _P], _I),
+    "th_capture_begin": ([_P], _I),
+    "th_capture_end": ([_P, _P], _I),
+    "th_graph_launch": ([_P], _I),
+    "th_graph_destroy": ([_P], _I),
     "th_buffer_alloc": ([_P, _I, _S, _P], _I),
     "th_buffer_free": ([_P], _I),
     "th_buffer_upload": ([_P, _P, _S], _I),
@@ -369,6 +373,27 @@ class Sampler:
             pass
 
 
+class Graph:
+    """A captured sequence of library calls, replayed with launch()."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def launch(self):
+        check(lib().th_graph_launch(self.handle))
+
+    def free(self):
+        if self.handle:
+            lib().th_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class HipComputeDevice:
     """One device handle (one HIP stream), methods named as ComputeDevice's."""
 
@@ -416,6 +441,18 @@ class HipComputeDevice:
         ms = ctypes.c_float()
         check(lib().th_timer_stop(self.handle, ctypes.byref(ms)))
         return ms.value
+
+    def capture(self, fn):
+        """Record the library calls fn() makes on this device's stream into a
+        Graph (th_capture_begin / th_capture_end)."""
+        check(lib().th_capture_begin(self.handle))
+        try:
+            fn()
+        finally:
+            h = ctypes.c_void_p()
+            rc = lib().th_capture_end(self.handle, ctypes.byref(h))
+        check(rc)
+        return Graph(h)
 
     # -- quantized weights
     def q4_upload_blocks(self, blocks, rows, cols, scale_dtype=F32):

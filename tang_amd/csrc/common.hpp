@@ -102,6 +102,12 @@ inline void device_drain(th_device* d) {
     if (!d->closed) (void)hipStreamSynchronize(d->stream);
 }
 
+// A captured sequence of library calls (th_capture_begin / th_capture_end).
+struct th_graph {
+    th_device* dev = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
 struct th_buffer {
     th_device* dev = nullptr;
     th_dtype dtype = TH_F32;

@@ -315,6 +315,48 @@ int th_timer_stop(th_device* d, float* ms) {
     TH_API_END
 }
 
+int th_capture_begin(th_device* d) {
+    TH_API_BEGIN
+    TH_REQUIRE(d, "null device");
+    TH_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+    TH_API_END
+}
+
+int th_capture_end(th_device* d, th_graph** out) {
+    TH_API_BEGIN
+    TH_REQUIRE(d && out, "null argument");
+    hipGraph_t g = nullptr;
+    TH_HIP(hipStreamEndCapture(d->stream, &g));
+    hipGraphExec_t ge = nullptr;
+    const hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    TH_HIP(e);
+    th_graph* r = new th_graph();
+    r->dev = d;
+    r->exec = ge;
+    device_retain(d);
+    *out = r;
+    TH_API_END
+}
+
+int th_graph_launch(th_graph* g) {
+    TH_API_BEGIN
+    TH_REQUIRE(g && !g->dev->closed, "null graph or closed device");
+    TH_HIP(hipGraphLaunch(g->exec, g->dev->stream));
+    TH_API_END
+}
+
+int th_graph_destroy(th_graph* g) {
+    TH_API_BEGIN
+    if (!g) return TH_OK;
+    device_drain(g->dev);
+    (void)hipGraphExecDestroy(g->exec);
+    th_device* d = g->dev;
+    delete g;
+    device_release(d);
+    TH_API_END
+}
+
 int th_buffer_alloc(th_device* d, th_dtype dt, size_t n, th_buffer** out) {
     TH_API_BEGIN
     TH_REQUIRE(d && out, "null argument");

@@ -147,6 +147,10 @@ constexpr int MLA_WMAX = 576;
 constexpr int MLA_WAVES = 8;                                 // 512 threads, two waves per SIMD
 constexpr int MLA_THREADS = 64 * MLA_WAVES;
 constexpr int MLA_NT = 512 / 16 / MLA_WAVES;                 // P.C output tiles of 16 latent dims per wave
+constexpr int MLA_PS = MLA_CHUNK + 4;                        // P row stride: 16-byte rows, 8 heads in distinct banks
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 // W = r + dr is a template parameter (a multiple of 32 up to 576) so that
 // every index below is a constant expression.
@@ -162,7 +166,6 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
     uint16_t* cs = (uint16_t*)lds_raw;                         // [MLA_CHUNK][WP]
     float* sred = (float*)(cs + (size_t)MLA_CHUNK * WP);        // [MLA_WAVES][MLA_H][MLA_CHUNK] partial scores
     float* ps = sred + MLA_WAVES * MLA_H * MLA_CHUNK;           // [MLA_H][MLA_PS] probabilities
-    constexpr int MLA_PS = MLA_CHUNK + 1;                       // odd stride: the 16 heads in different banks
     __shared__ float m_run[MLA_H], l_run[MLA_H], resc[MLA_H];
     const int b = blockIdx.x, s = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
         // its own value, and the last chunk "prefetches" itself (L2 hits)
 #pragma unroll
         for (int u = 0; u < PPT; u++) *(u32x4_t*)(cs + (size_t)prow[u] * WP + pcol[u]) = pre[u];
-        __syncthreads();
+        lds_barrier();  // LDS only: the next chunk's loads stay in flight across it
         {
             const int cn = p0 + min(c + 1, nch - 1) * MLA_CHUNK;
 #pragma unroll
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
         for (int pt = 0; pt < 4; pt++)
 #pragma unroll
             for (int j = 0; j < 4; j++) sred[(wave * MLA_H + 4 * q + j) * MLA_CHUNK + pt * 16 + r] = d[pt][j];
-        __syncthreads();
+        lds_barrier();
         // softmax step: thread (head hh, positions 2 pg, 2 pg + 1); 32 threads per head
         {
             const int hh = tid >> 5, pg = tid & 31;
@@ -252,8 +255,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
                 sv[j] = p < clen ? v * sm_scale : -INFINITY;
                 cmax = fmaxf(cmax, sv[j]);
             }
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, o, 64));
+            cmax = group_max<32>(cmax);
             const float mold = m_run[hh];
             const float mnew = fmaxf(mold, cmax);
             float lsum = 0.0f;
@@ -263,9 +265,8 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
                 ps[hh * MLA_PS + 2 * pg + j] = e;
                 lsum += e;
             }
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
-            __syncthreads();  // every thread has read m_run
+            lsum = group_sum<32>(lsum);
+            lds_barrier();  // every thread has read m_run
             if (pg == 0) {
                 const float f = expf(mold - mnew);
                 resc[hh] = f;
@@ -273,16 +274,18 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
                 m_run[hh] = mnew;
             }
         }
-        __syncthreads();
-        // P.C: D[head][latent dim] += P[head][pos] C[pos][dim].  MFMA k index
-        // 8q + j of step kk stands for position 8j + 2q + kk: the four lane
-        // groups then read cache rows 2 apart (8 banks apart), not 8 apart.
+        lds_barrier();
+        // P.C: D[head][latent dim] += P[head][pos] C[pos][dim], MFMA k index
+        // 8q + e of step kk = position 32 kk + 8q + e.  A: lane (q, r) holds
+        // P[head r][32 kk + 8q ..+8); B: two transposing LDS reads, each
+        // giving lane (q, r) C[32 kk + 8q + 4 hf ..+4][d0 + r] (the 16 lanes
+        // of a row group address four rows of four dims each).
         uint4 ahi[2], alo[2];
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
-            float pv[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) pv[j] = ps[r * MLA_PS + 8 * j + 2 * q + kk];
+            const float4 pa = *(const float4*)&ps[r * MLA_PS + 32 * kk + 8 * q];
+            const float4 pb = *(const float4*)&ps[r * MLA_PS + 32 * kk + 8 * q + 4];
+            const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
             uint32_t h2[4], l2[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -304,14 +307,17 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
             const int d0 = min((wave * MLA_NT + nt) * 16, R - 16);  // tiles past r: computed, not stored
 #pragma unroll
             for (int kk = 0; kk < 2; kk++) {
-                uint32_t bw[4];
+                short4_t t[2];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint32_t x0 = cs[(size_t)(16 * e + 2 * q + kk) * WP + d0 + r];
-                    const uint32_t x1 = cs[(size_t)(16 * e + 8 + 2 * q + kk) * WP + d0 + r];
-                    bw[e] = x0 | (x1 << 16);
+                for (int hf = 0; hf < 2; hf++) {
+                    const int row = 32 * kk + 8 * q + 4 * hf + (r >> 2);
+                    t[hf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_short4_t*)(cs + (size_t)row * WP + d0 + 4 * (r & 3)));
                 }
-                bq[nt][kk] = make_uint4(bw[0], bw[1], bw[2], bw[3]);
+                bq[nt][kk] = make_uint4((uint16_t)t[0][0] | ((uint32_t)(uint16_t)t[0][1] << 16),
+                                        (uint16_t)t[0][2] | ((uint32_t)(uint16_t)t[0][3] << 16),
+                                        (uint16_t)t[1][0] | ((uint32_t)(uint16_t)t[1][1] << 16),
+                                        (uint16_t)t[1][2] | ((uint32_t)(uint16_t)t[1][3] << 16));
             }
         }
 #pragma unroll
@@ -326,7 +332,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
                                                                   __builtin_bit_cast(bf16x8_t, bq[nt][kk]), acc[nt], 0, 0, 0);
             }
         }
-        __syncthreads();  // cs, sred and ps are rewritten by the next chunk
+        lds_barrier();  // cs, sred and ps are rewritten by the next chunk
     }
     // record per head: {m, l, acc[R]}; lane (q, r) holds heads 4q..4q+3 of dim d0 + r
     // (plain stores: the merge is the next launch)
@@ -512,7 +518,7 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     TH_LAUNCH_CHECK();
     // 2. latent attention
     const size_t lds = (size_t)MLA_CHUNK * (W + 8) * 2 + (size_t)MLA_WAVES * MLA_H * MLA_CHUNK * 4 +
-                       (size_t)MLA_H * (MLA_CHUNK + 1) * 4;
+                       (size_t)MLA_H * MLA_PS * 4;
     TH_REQUIRE(lds <= 150 * 1024, "latent chunk does not fit LDS");
     launch_mla_attn(W, dim3((unsigned)B, (unsigned)n_splits), lds, s, qa, (const uint16_t*)cache->ptr, (int)L, (int)r,
                     sm_scale, n_splits, part);

@@ -66,6 +66,10 @@ pub struct th_sampler {
 pub struct th_moe {
     _private: [u8; 0],
 }
+#[repr(C)]
+pub struct th_graph {
+    _private: [u8; 0],
+}
 
 /// `Q8Block` (crates/tang-infer/src/quantize.rs:15-19) as a C struct.
 #[repr(C)]
@@ -120,6 +124,10 @@ extern "C" {
     pub fn th_memory_info(dev: *mut th_device, free_bytes: *mut usize, total_bytes: *mut usize) -> c_int;
     pub fn th_timer_start(dev: *mut th_device) -> c_int;
     pub fn th_timer_stop(dev: *mut th_device, ms: *mut f32) -> c_int;
+    pub fn th_capture_begin(dev: *mut th_device) -> c_int;
+    pub fn th_capture_end(dev: *mut th_device, out: *mut *mut th_graph) -> c_int;
+    pub fn th_graph_launch(g: *mut th_graph) -> c_int;
+    pub fn th_graph_destroy(g: *mut th_graph) -> c_int;
     pub fn th_buffer_alloc(dev: *mut th_device, dtype: c_int, n: usize, out: *mut *mut th_buffer) -> c_int;
     pub fn th_buffer_free(buf: *mut th_buffer) -> c_int;
     pub fn th_buffer_upload(buf: *mut th_buffer, host: *const c_void, n: usize) -> c_int;

@@ -52,6 +52,36 @@ def test_mla_small_latent_and_repeat(dev):
         assert max_abs_rel(out, ref) < TOL
 
 
+def test_mla_graph_replay_matches_eager(dev):
+    """th_capture_begin/end around two calls, replayed three times with eager
+    calls and synchronisations between the replays: every replay gives the
+    eager outputs bit for bit (same kernels, same buffers)."""
+    B, L = 2, 700
+    qn, qr, cache, wuk, suk, wuv, suv = _case(11, B, L)
+    wk = dev.q8_upload_rowwise(wuk, suk, H * R, DN)
+    wv = dev.q8_upload_rowwise(wuv, suv, H * DV, R)
+    bq, br, bc = dev.upload(qn), dev.upload(qr), dev.upload(cache, capi.BF16)
+    bq2 = dev.upload(capi.synth_normal(99, B * H * DN, 1.0, capi.F32))
+    scale = 1.0 / np.sqrt(DN + DR)
+    out1, out2 = dev.alloc(B * H * DV), dev.alloc(B * H * DV)
+    dev.mla_decode(bq, br, bc, B, H, L, DN, DR, R, DV, wk, wv, scale, out1)
+    dev.mla_decode(bq2, br, bc, B, H, L, DN, DR, R, DV, wk, wv, scale, out2)
+    e1, e2 = out1.to_numpy().copy(), out2.to_numpy().copy()
+    g = dev.capture(lambda: (dev.mla_decode(bq, br, bc, B, H, L, DN, DR, R, DV, wk, wv, scale, out1),
+                             dev.mla_decode(bq2, br, bc, B, H, L, DN, DR, R, DV, wk, wv, scale, out2)))
+    try:
+        for rep in range(3):
+            out1.upload(np.zeros(B * H * DV, np.float32))
+            out2.upload(np.zeros(B * H * DV, np.float32))
+            g.launch()
+            dev.sync()
+            assert np.array_equal(out1.to_numpy(), e1) and np.array_equal(out2.to_numpy(), e2), rep
+            dev.mla_decode(bq2, br, bc, B, H, L, DN, DR, R, DV, wk, wv, scale, out1)  # eager work between replays
+            dev.sync()
+    finally:
+        g.free()
+
+
 def test_mla_rejects_bad_shapes(dev):
     qn, qr, cache, wuk, suk, wuv, suv = _case(1, 1, 8)
     wk = dev.q8_upload_rowwise(wuk, suk, H * R, DN)
