@@ -7,18 +7,20 @@
 //   o_lat[b,h] = sum_t softmax_t(s) c[b,t,:r]
 //   out[b,h]   = W_UV[h] . o_lat[b,h]                 (int8, per-row scale)
 // Three launches:
-//   1. absorb: q = [q_lat ; q_rope] (f32) emitted as hi + lo bf16 parts
-//      (16 significant bits) as the MFMA A operand [B][2][H][r+dr];
+//   1. absorb on MFMA (one wave per 16 W_UK rows, every sequence at once):
+//      q = [q_lat ; q_rope] (f32) emitted as hi + lo bf16 parts (16
+//      significant bits) as the attention's MFMA A operand [B][2][H][r+dr];
 //   2. one workgroup per (sequence, split of 128 positions) serves all 16
 //      heads from one pass over the latent cache, in chunks of 64 positions
 //      staged in LDS (the next chunk is loaded into registers meanwhile):
 //      scores on v_mfma_f32_16x16x32_bf16 (heads x positions; each wave owns
 //      a quarter of the k-steps and keeps its A operand in registers; partial
 //      scores are summed in LDS), online softmax per head, then P.C on the
-//      same MFMA (P as hi + lo bf16, C exact bf16), one {max, sum, o_lat}
+//      same MFMA (P as hi + lo bf16, C exact bf16, read with transposing LDS
+//      reads), one {max, sum, o_lat}
 //      record per split;
-//   3. per (head, sequence): the split merge in LDS, then the up-projection
-//      through W_UV.
+//   3. per (head, sequence, 64 output rows): the split merge in LDS, then
+//      the up-projection through W_UV on MFMA.
 // The cache dominates the traffic: B*L*(r+dr)*2 bytes.
 #include <mutex>
 #include <utility>
@@ -33,108 +35,88 @@ constexpr int MLA_H = 16;       // heads per MFMA row block (config 5: 16)
 constexpr int MLA_CHUNK = 64;   // positions staged per pass
 constexpr int MLA_SPLIT = 128;  // positions per workgroup
 
-// Per-head batched int8 GEMV over the tiled q8 layout (16 rows x 64 k per
-// tile, lane q*16+r holds k 16q..16q+15 of row r), per-row scales:
-// y[b][h][n] = scale[h*rows+n] * sum_k q[h*rows+n][k] * x[b][h][k].
-// One workgroup: head h, 16 output rows, all B inputs.  Thread (row r,
-// slice kq) owns the 16-value pieces kq, kq+16, ... of its row: every weight
-// byte is loaded once, up front; partial sums meet in LDS.
-constexpr int MLA_GEMV_PIECES = 4;  // pieces per thread: K <= 1024
-constexpr int MLA_GEMV_X4 = 8;      // float4 activation loads per thread: B * K <= 8192
+// Absorb on MFMA: q_lat[b][h][n] = scale[h*R+n] * sum_k W_UK[h*R+n][k] x[b][h][k]
+// for every sequence b at once.  One wave per 16-row tile of the stacked
+// W_UK (q8 tiles: 16 rows x 64 k, lane q*16+r holding k 16q..16q+15 of row
+// r): A = x (rows = sequences, at most 16, as hi + lo bf16 parts), B = the
+// tile's int8 weights as bf16 (exact), v_mfma_f32_16x16x32_bf16 per half of
+// a lane's 16 k (MFMA k index 8q + e of step (c, hh) = k c*64 + 16q + 8hh + e),
+// so lane (q, r) ends with sequences 4q..4q+3 of row r.  Output: the
+// attention's A operand [B][2][H][r+dr] (hi, lo bf16), q_rope copied in.
+constexpr int MLA_ABS_CH = 4;  // 64-k chunks of W_UK: qk_nope width <= 256
 
-template <int MODE>  // 0: absorb (write the hi / lo bf16 A operand), 1: plain f32 out
-__global__ __launch_bounds__(256) void mla_q8_heads_kernel(const uint8_t* __restrict__ wq, const float* __restrict__ wsc,
-                                                           int rows_per_head, int K, int Kp, int B, int H,
-                                                           const float* __restrict__ x, int ldx_b, int ldx_h,
-                                                           float* __restrict__ y, uint16_t* __restrict__ qa,
-                                                           const float* __restrict__ q_rope, int dr) {
-    extern __shared__ float sm[];
-    const int NP = Kp >> 4, NCH = Kp >> 6;
-    float* xs = sm;                          // [B][NP][20]: piece-major; the pad puts a wave's 4 slices in different banks
-    float* red = sm + (size_t)B * NP * 20;   // [B][16 slices][16 rows]
-    const int h = blockIdx.x, t_local = blockIdx.y, tid = threadIdx.x;
-    const int r = tid & 15, kq = tid >> 4;
-    const int row = h * rows_per_head + t_local * 16 + r;  // row of the stacked matrix
-    const int t = row >> 4;                                // its 16-row tile
-    uint4 w[MLA_GEMV_PIECES];
+__global__ __launch_bounds__(256) void mla_absorb_kernel(const uint8_t* __restrict__ wq, const float* __restrict__ wsc,
+                                                         int R, int dn, int nch, int B, const float* __restrict__ x,
+                                                         const float* __restrict__ q_rope, int dr,
+                                                         uint16_t* __restrict__ qa) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, r = lane & 15;
+    const int TT = MLA_H * R / 16, W = R + dr;
+    const int t = min((int)blockIdx.x * 4 + wave, TT - 1);  // surplus waves redo the last tile, store nothing
+    const int h = 16 * t / R;
+    uint4 w[MLA_ABS_CH];
 #pragma unroll
-    for (int j = 0; j < MLA_GEMV_PIECES; j++) {
-        const int p = min(kq + 16 * j, NP - 1);  // surplus pieces: loaded, not used
-        w[j] = *(const uint4*)(wq + (((size_t)t * NCH + (p >> 2)) * 64 + (p & 3) * 16 + r) * 16);
-    }
-    const float sc = wsc[row];
-    // activations: float4 pieces, every load issued before any is used (a
-    // loop of load-then-store would wait out one latency per iteration);
-    // surplus threads repeat the last piece, k >= K is zero
-    {
-        const int K4 = Kp >> 2, n4 = B * K4;
-        float4 xv[MLA_GEMV_X4];
+    for (int c = 0; c < MLA_ABS_CH; c++) w[c] = *(const uint4*)(wq + (((size_t)t * nch + min(c, nch - 1)) * 64 + lane) * 16);
+    // sequence r's activations (rows r >= B are zero): k = c*64 + 16q + 8hh + e
+    float4 xv[MLA_ABS_CH][2][2];
+    const float* xr = x + ((size_t)min(r, B - 1) * MLA_H + h) * dn;
 #pragma unroll
-        for (int u = 0; u < MLA_GEMV_X4; u++) {
-            const int i = min(tid + 256 * u, n4 - 1);
-            const int b = i / K4, k = (i - b * K4) * 4;
-            xv[u] = *(const float4*)(x + (size_t)b * ldx_b + (size_t)h * ldx_h + min(k, K - 4));
-            if (k >= K) xv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int c = 0; c < MLA_ABS_CH; c++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int f = 0; f < 2; f++) xv[c][hh][f] = *(const float4*)(xr + min(c * 64 + 16 * q + 8 * hh + 4 * f, dn - 4));
+    float4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < MLA_ABS_CH; c++) {
+        if (c >= nch) break;
+        const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            uint32_t bw[4], ah[4], al[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t word = ww[2 * hh + (e >> 1)];
+                const int sh = 16 * (e & 1);
+                const float w0 = (float)(int8_t)(word >> sh), w1 = (float)(int8_t)(word >> (sh + 8));
+                bw[e] = (__float_as_uint(w0) >> 16) | (__float_as_uint(w1) & 0xFFFF0000u);  // exact: |w| <= 127
+                const float4 xf = xv[c][hh][e >> 1];
+                const int k0 = c * 64 + 16 * q + 8 * hh + 2 * e;
+                const bool live = r < B;
+                const float x0 = live && k0 < dn ? ((e & 1) ? xf.z : xf.x) : 0.0f;
+                const float x1 = live && k0 + 1 < dn ? ((e & 1) ? xf.w : xf.y) : 0.0f;
+                const uint32_t h0 = f32_to_bf16_bits(x0), h1 = f32_to_bf16_bits(x1);
+                ah[e] = h0 | (h1 << 16);
+                al[e] = f32_to_bf16_bits(x0 - bf16_bits_to_f32(h0)) | (f32_to_bf16_bits(x1 - bf16_bits_to_f32(h1)) << 16);
+            }
+            const bf16x8_t B8 = __builtin_bit_cast(bf16x8_t, make_uint4(bw[0], bw[1], bw[2], bw[3]));
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(ah[0], ah[1], ah[2], ah[3])),
+                                                        B8, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(al[0], al[1], al[2], al[3])),
+                                                        B8, d, 0, 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < MLA_GEMV_X4; u++) {
-            const int i = min(tid + 256 * u, n4 - 1);
-            const int b = i / K4, k = (i - b * K4) * 4;
-            *(float4*)(xs + (b * NP + (k >> 4)) * 20 + (k & 15)) = xv[u];
-        }
     }
-    // weights as f32 once (surplus pieces contribute zero)
-    float wf[MLA_GEMV_PIECES][16];
+    if ((int)blockIdx.x * 4 + wave < TT) {
+        const int row = 16 * t + r, n = row - h * R;
+        const float sc = wsc[row];
 #pragma unroll
-    for (int j = 0; j < MLA_GEMV_PIECES; j++) {
-        const bool live = kq + 16 * j < NP;
-        const uint32_t wj[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
-#pragma unroll
-        for (int e = 0; e < 16; e++) wf[j][e] = live ? (float)(int8_t)(wj[e >> 2] >> (8 * (e & 3))) : 0.0f;
-    }
-    __syncthreads();
-    for (int b = 0; b < B; b++) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < MLA_GEMV_PIECES; j++) {
-            const float4* xp = (const float4*)(xs + (b * NP + min(kq + 16 * j, NP - 1)) * 20);
-#pragma unroll
-            for (int e4 = 0; e4 < 4; e4++) {
-                const float4 xv = xp[e4];
-                acc = __builtin_fmaf(wf[j][4 * e4], xv.x, acc);
-                acc = __builtin_fmaf(wf[j][4 * e4 + 1], xv.y, acc);
-                acc = __builtin_fmaf(wf[j][4 * e4 + 2], xv.z, acc);
-                acc = __builtin_fmaf(wf[j][4 * e4 + 3], xv.w, acc);
+        for (int j = 0; j < 4; j++) {
+            const int b = 4 * q + j;
+            if (b < B) {
+                const float v = d[j] * sc;
+                const uint32_t hi = f32_to_bf16_bits(v);
+                qa[(((size_t)b * 2 + 0) * MLA_H + h) * W + n] = (uint16_t)hi;
+                qa[(((size_t)b * 2 + 1) * MLA_H + h) * W + n] = (uint16_t)f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
             }
         }
-        red[(b * 16 + kq) * 16 + r] = acc;
     }
-    __syncthreads();
-    if (tid >= 16 * B) return;
-    const int b = tid >> 4;  // r = tid & 15 as above
-    float v = 0.0f;
-#pragma unroll
-    for (int k2 = 0; k2 < 16; k2++) v += red[(b * 16 + k2) * 16 + r];
-    v *= sc;
-    const int n = t_local * 16 + r;
-    if (MODE == 0) {
-        // A operand row (b, part, h): q_lat then q_rope, as hi / lo parts
-        const int R = rows_per_head, W = R + dr;
-        const uint32_t hi = f32_to_bf16_bits(v);
-        const uint32_t lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
-        qa[(((size_t)b * 2 + 0) * H + h) * W + n] = (uint16_t)hi;
-        qa[(((size_t)b * 2 + 1) * H + h) * W + n] = (uint16_t)lo;
-        if (t_local == 0) {
-            for (int i = r; i < dr; i += 16) {
-                const float qr = q_rope[((size_t)b * H + h) * dr + i];
-                const uint32_t h2 = f32_to_bf16_bits(qr);
-                const uint32_t l2 = f32_to_bf16_bits(qr - bf16_bits_to_f32(h2));
-                qa[(((size_t)b * 2 + 0) * H + h) * W + R + i] = (uint16_t)h2;
-                qa[(((size_t)b * 2 + 1) * H + h) * W + R + i] = (uint16_t)l2;
-            }
-        }
-    } else {
-        y[((size_t)b * H + h) * rows_per_head + n] = v;
+    // q_rope, split over the grid
+    for (int j = blockIdx.x * 256 + tid; j < B * MLA_H * dr; j += gridDim.x * 256) {
+        const int bh = j / dr, i = j - bh * dr, b = bh / MLA_H, hh = bh - b * MLA_H;
+        const float qr = q_rope[j];
+        const uint32_t h2 = f32_to_bf16_bits(qr);
+        qa[(((size_t)b * 2 + 0) * MLA_H + hh) * W + R + i] = (uint16_t)h2;
+        qa[(((size_t)b * 2 + 1) * MLA_H + hh) * W + R + i] = (uint16_t)f32_to_bf16_bits(qr - bf16_bits_to_f32(h2));
     }
 }
 
@@ -166,7 +148,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
     uint16_t* cs = (uint16_t*)lds_raw;                         // [MLA_CHUNK][WP]
     float* sred = (float*)(cs + (size_t)MLA_CHUNK * WP);        // [MLA_WAVES][MLA_H][MLA_CHUNK] partial scores
     float* ps = sred + MLA_WAVES * MLA_H * MLA_CHUNK;           // [MLA_H][MLA_PS] probabilities
-    __shared__ float m_run[MLA_H], l_run[MLA_H], resc[MLA_H];
+    __shared__ float resc[MLA_H];
     const int b = blockIdx.x, s = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r = lane & 15;
@@ -204,7 +186,8 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
     float4_t acc[MLA_NT];
 #pragma unroll
     for (int nt = 0; nt < MLA_NT; nt++) acc[nt] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
-    if (tid < MLA_H) { m_run[tid] = -INFINITY; l_run[tid] = 0.0f; }
+    // running max and sum of head tid >> 5, kept alike by its 32 softmax threads
+    float m_run = -INFINITY, l_run = 0.0f;
 
     for (int c = 0; c < nch; c++) {
         const int clen = min(MLA_CHUNK, len - c * MLA_CHUNK);
@@ -226,15 +209,15 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
 #pragma unroll
         for (int i = 0; i < KSW; i++) {
             const int ks = min(wave + MLA_WAVES * i, KS - 1);
-            uint4 bq[4];
+            uint4 bs[4];
 #pragma unroll
-            for (int pt = 0; pt < 4; pt++) bq[pt] = *(const uint4*)(cs + (size_t)(pt * 16 + r) * WP + ks * 32 + q * 8);
+            for (int pt = 0; pt < 4; pt++) bs[pt] = *(const uint4*)(cs + (size_t)(pt * 16 + r) * WP + ks * 32 + q * 8);
 #pragma unroll
             for (int pp = 0; pp < 2; pp++)
 #pragma unroll
                 for (int pt = 0; pt < 4; pt++)
                     d[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, areg[i][pp]),
-                                                                    __builtin_bit_cast(bf16x8_t, bq[pt]), d[pt], 0, 0, 0);
+                                                                    __builtin_bit_cast(bf16x8_t, bs[pt]), d[pt], 0, 0, 0);
         }
 #pragma unroll
         for (int pt = 0; pt < 4; pt++)
@@ -256,7 +239,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
                 cmax = fmaxf(cmax, sv[j]);
             }
             cmax = group_max<32>(cmax);
-            const float mold = m_run[hh];
+            const float mold = m_run;
             const float mnew = fmaxf(mold, cmax);
             float lsum = 0.0f;
 #pragma unroll
@@ -266,13 +249,10 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
                 lsum += e;
             }
             lsum = group_sum<32>(lsum);
-            lds_barrier();  // every thread has read m_run
-            if (pg == 0) {
-                const float f = expf(mold - mnew);
-                resc[hh] = f;
-                l_run[hh] = l_run[hh] * f + lsum;
-                m_run[hh] = mnew;
-            }
+            const float f = expf(mold - mnew);
+            if (pg == 0) resc[hh] = f;
+            l_run = l_run * f + lsum;
+            m_run = mnew;
         }
         lds_barrier();
         // P.C: D[head][latent dim] += P[head][pos] C[pos][dim], MFMA k index
@@ -344,42 +324,40 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
 #pragma unroll
             for (int j = 0; j < 4; j++) rec[(size_t)(4 * q + j) * (R + 2) + 2 + d0 + r] = acc[nt][j];
     }
-    if (tid < MLA_H) {
-        rec[(size_t)tid * (R + 2)] = m_run[tid];
-        rec[(size_t)tid * (R + 2) + 1] = l_run[tid];
+    if ((tid & 31) == 0) {
+        rec[(size_t)(tid >> 5) * (R + 2)] = m_run;
+        rec[(size_t)(tid >> 5) * (R + 2) + 1] = l_run;
     }
 }
 
 // Split merge fused with the W_UV up-projection: workgroup (head h,
-// sequence b).  o_lat[b][h] = sum_s w_s acc_s / sum_s w_s l_s (split order,
-// w_s = exp(m_s - max m)) is built in LDS, then out[b][h][n] = scale_n *
-// sum_k W_UV[h*dv + n][k] o_lat[k]: thread (row n, half of the 64-k chunks),
-// halves summed in order; the W_UV and record loads are all issued at the
-// start.  r <= 512, dv <= 128, n_splits <= 64.
+// sequence b, row group g).  o_lat[b][h] = sum_s w_s acc_s / sum_s w_s l_s
+// (split order, w_s = exp(m_s - max m)) is built in LDS, then each wave
+// takes one 16-row tile of the head's W_UV rows on MFMA, as the absorb:
+// A = o_lat (row 0; hi + lo bf16), B = the tile's int8 weights as bf16,
+// MFMA k index 8q + e of step (c, hh) = k c*64 + 16q + 8hh + e.  The W_UV
+// and record loads are all issued at the start.  r <= 512, dv <= 128,
+// n_splits <= 64.
 constexpr int MLA_UP_THREADS = 256;
+constexpr int MLA_UP_CH = 8;  // 64-k chunks of W_UV: r <= 512
 
 __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const float* __restrict__ part, int n_splits,
                                                                      int R, const uint8_t* __restrict__ wq,
-                                                                     const float* __restrict__ wsc, int dv, int Kp,
+                                                                     const float* __restrict__ wsc, int dv, int nch,
                                                                      float* __restrict__ out) {
     __shared__ __align__(16) float olat[512];
     __shared__ float wts[64];
     __shared__ float Lsh;
-    __shared__ float half_sum[2][128];
-    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y, g = blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), q = lane >> 4, r = lane & 15;
     const float* recs = part + (size_t)b * n_splits * MLA_H * (R + 2);
-    constexpr int DPT = 2, SB = 32;    // dims per thread, splits per load round
-    constexpr int CPT = 4;             // 64-k chunks of W_UV per thread (r <= 512)
-    // the up-projection's weights do not depend on the merge: load them first
-    const int n = tid & 127, kh = tid >> 7, NCH = Kp >> 6;
-    const int row = h * dv + min(n, dv - 1), t = row >> 4, r = row & 15;
-    uint4 w4[CPT][4];
+    constexpr int DPT = 2, SB = 32;  // dims per thread, splits per load round
+    // this wave's W_UV tile first: it does not depend on the merge
+    const int TV = dv / 16, tt = g * 4 + wave;
+    const int trow = h * TV + min(tt, TV - 1);  // 16-row tile of the stacked W_UV
+    uint4 w[MLA_UP_CH];
 #pragma unroll
-    for (int ci = 0; ci < CPT; ci++) {
-        const int c = min(kh * CPT + ci, NCH - 1);  // chunks past K: loaded, multiplied by zero below
-#pragma unroll
-        for (int q = 0; q < 4; q++) w4[ci][q] = *(const uint4*)(wq + (((size_t)t * NCH + c) * 64 + q * 16 + r) * 16);
-    }
+    for (int c = 0; c < MLA_UP_CH; c++) w[c] = *(const uint4*)(wq + (((size_t)trow * nch + min(c, nch - 1)) * 64 + lane) * 16);
     float v[SB][DPT];
 #pragma unroll
     for (int i = 0; i < SB; i++)
@@ -393,9 +371,9 @@ __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const floa
         float M = m;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-        const float w = tid < n_splits ? expf(m - M) : 0.0f;
-        const float L = wave_sum(w * l);
-        wts[tid] = w;
+        const float wgt = tid < n_splits ? expf(m - M) : 0.0f;
+        const float L = wave_sum(wgt * l);
+        wts[tid] = wgt;
         if (tid == 0) Lsh = L;
     }
     __syncthreads();
@@ -418,31 +396,42 @@ __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const floa
 #pragma unroll
     for (int j = 0; j < DPT; j++) olat[tid + 256 * j] = tid + 256 * j < R ? a[j] / Lsh : 0.0f;
     __syncthreads();
-    // out[n] = scale_n * sum_k W_UV[n][k] o_lat[k]; thread (row n, half kh of the chunks)
-    float acc = 0.0f;
+    if (tt >= TV) return;  // wave-uniform: no barrier follows
+    float4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int ci = 0; ci < CPT; ci++) {
-        const int c = kh * CPT + ci;
+    for (int c = 0; c < MLA_UP_CH; c++) {
+        if (c >= nch) break;
+        const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint32_t ww[4] = {w4[ci][q].x, w4[ci][q].y, w4[ci][q].z, w4[ci][q].w};
+        for (int hh = 0; hh < 2; hh++) {
+            // o_lat as A row 0 (the other rows zero): k = c*64 + 16q + 8hh + e
+            const float4 o0 = *(const float4*)&olat[min(c * 64 + 16 * q + 8 * hh, 504)];
+            const float4 o1 = *(const float4*)&olat[min(c * 64 + 16 * q + 8 * hh + 4, 508)];
+            const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+            uint32_t bw[4], ah[4], al[4];
 #pragma unroll
-            for (int e4 = 0; e4 < 4; e4++) {
-                const int k0 = c * 64 + q * 16 + e4 * 4;  // olat is zero past R (cleared below), 512 entries
-                const float4 o = (c < NCH) ? *(const float4*)&olat[min(k0, 508)] : make_float4(0.f, 0.f, 0.f, 0.f);
-                const float ov[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    acc = __builtin_fmaf((float)(int8_t)(ww[e4] >> (8 * e)), ov[e], acc);
+            for (int e = 0; e < 4; e++) {
+                const uint32_t word = ww[2 * hh + (e >> 1)];
+                const int sh = 16 * (e & 1);
+                const float w0 = (float)(int8_t)(word >> sh), w1 = (float)(int8_t)(word >> (sh + 8));
+                bw[e] = (__float_as_uint(w0) >> 16) | (__float_as_uint(w1) & 0xFFFF0000u);  // exact: |w| <= 127
+                const float x0 = r == 0 ? ov[2 * e] : 0.0f, x1 = r == 0 ? ov[2 * e + 1] : 0.0f;
+                const uint32_t h0 = f32_to_bf16_bits(x0), h1 = f32_to_bf16_bits(x1);
+                ah[e] = h0 | (h1 << 16);
+                al[e] = f32_to_bf16_bits(x0 - bf16_bits_to_f32(h0)) | (f32_to_bf16_bits(x1 - bf16_bits_to_f32(h1)) << 16);
             }
+            const bf16x8_t B8 = __builtin_bit_cast(bf16x8_t, make_uint4(bw[0], bw[1], bw[2], bw[3]));
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(ah[0], ah[1], ah[2], ah[3])),
+                                                        B8, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(al[0], al[1], al[2], al[3])),
+                                                        B8, d, 0, 0, 0);
         }
     }
-    half_sum[kh][n] = acc;
-    __syncthreads();
-    if (tid < dv) out[((size_t)b * MLA_H + h) * dv + tid] = (half_sum[0][tid] + half_sum[1][tid]) * wsc[h * dv + tid];
+    if (q == 0) {  // D[row 0][col r]: lane (0, r), element 0
+        const int n = tt * 16 + r;
+        out[((size_t)b * MLA_H + h) * dv + n] = d[0] * wsc[h * dv + n];
+    }
 }
-
-static size_t head_gemv_lds(size_t B, size_t Kp) { return (B * (Kp / 16) * 20 + B * 256) * 4; }
 
 template <int W>
 static void launch_mla_attn_w(dim3 grid, size_t lds, hipStream_t s, const uint16_t* qa, const uint16_t* cache, int L,
@@ -502,8 +491,7 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     const size_t W = r + dr;
     const int n_splits = (int)ceil_div(L, (size_t)MLA_SPLIT);
     TH_REQUIRE(n_splits <= 64, "L above 8192 positions");
-    TH_REQUIRE(dn % 4 == 0 && B * w_uk->Kp <= 8192 && B * w_uv->Kp <= 8192,
-               "qk_nope width must be a multiple of 4, and B * width <= 8192 for both projections");
+    TH_REQUIRE(dn % 4 == 0 && dn <= 64 * MLA_ABS_CH, "qk_nope width must be a multiple of 4, at most 256");
     // workspace: A operand, split records, o_lat
     const size_t qa_bytes = B * 2 * H * W * 2;
     const size_t part_bytes = B * (size_t)n_splits * H * (r + 2) * 4;
@@ -511,10 +499,9 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     uint16_t* qa = (uint16_t*)ws;
     float* part = (float*)(ws + round_up(qa_bytes, 256));
     // 1. absorb
-    hipLaunchKernelGGL(mla_q8_heads_kernel<0>, dim3((unsigned)H, (unsigned)(r / 16)), dim3(256), head_gemv_lds(B, w_uk->Kp), s,
-                       (const uint8_t*)w_uk->data, (const float*)w_uk->scales, (int)r, (int)dn, (int)w_uk->Kp, (int)B,
-                       (int)H, (const float*)q_nope->ptr, (int)(H * dn), (int)dn, (float*)nullptr, qa,
-                       (const float*)q_rope->ptr, (int)dr);
+    hipLaunchKernelGGL(mla_absorb_kernel, dim3((unsigned)ceil_div(H * r / 16, (size_t)4)), dim3(256), 0, s,
+                       (const uint8_t*)w_uk->data, (const float*)w_uk->scales, (int)r, (int)dn, (int)(w_uk->Kp / 64),
+                       (int)B, (const float*)q_nope->ptr, (const float*)q_rope->ptr, (int)dr, qa);
     TH_LAUNCH_CHECK();
     // 2. latent attention
     const size_t lds = (size_t)MLA_CHUNK * (W + 8) * 2 + (size_t)MLA_WAVES * MLA_H * MLA_CHUNK * 4 +
@@ -524,9 +511,10 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
                     sm_scale, n_splits, part);
     TH_LAUNCH_CHECK();
     // 3. merge + up-projection
-    hipLaunchKernelGGL(mla_merge_up_kernel, dim3((unsigned)H, (unsigned)B), dim3(MLA_UP_THREADS), 0, s, part, n_splits,
-                       (int)r, (const uint8_t*)w_uv->data, (const float*)w_uv->scales, (int)dv, (int)w_uv->Kp,
-                       (float*)out->ptr);
+    const unsigned groups = (unsigned)ceil_div(dv / 16, (size_t)4);  // four 16-row tiles per workgroup
+    hipLaunchKernelGGL(mla_merge_up_kernel, dim3((unsigned)H, (unsigned)B, groups), dim3(MLA_UP_THREADS), 0, s, part,
+                       n_splits, (int)r, (const uint8_t*)w_uv->data, (const float*)w_uv->scales, (int)dv,
+                       (int)(w_uv->Kp / 64), (float*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
 }
