@@ -465,14 +465,13 @@ __device__ __forceinline__ float4 moe_combine4(const float* __restrict__ y, cons
     return acc;
 }
 
-// Combine: one workgroup per token, each thread four consecutive outputs
+// Combine: workgroup (token, 1024 outputs), each thread four consecutive outputs
 // (moe_combine4).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y, const int* __restrict__ token_slot,
                                                           const float* __restrict__ topk_w, const int* __restrict__ offsets,
                                                           int k, int E, int S, int d, float* __restrict__ out) {
-    const int t = blockIdx.x;
-    for (int n = threadIdx.x * 4; n < d; n += 1024)
-        *(float4*)(out + (size_t)t * d + n) = moe_combine4(y, token_slot, topk_w, offsets, t, n, k, E, S, d);
+    const int t = blockIdx.x, n = (blockIdx.y * 256 + threadIdx.x) * 4;
+    if (n < d) *(float4*)(out + (size_t)t * d + n) = moe_combine4(y, token_slot, topk_w, offsets, t, n, k, E, S, d);
 }
 
 }  // namespace th
@@ -713,7 +712,7 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
                          max_work,
                          EpiGemmMoeStore{m->ybuf, (int)m->d});
     }
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, s, m->ybuf, m->token_slot,
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)ceil_div(m->d, (size_t)1024)), dim3(256), 0, s, m->ybuf, m->token_slot,
                        (const float*)topk_w->ptr, m->offsets, (int)m->k, (int)m->E, (int)m->S, (int)m->d,
                        (float*)out->ptr);
     TH_LAUNCH_CHECK();

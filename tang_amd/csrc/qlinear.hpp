@@ -731,13 +731,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     }
     for (int tt = 0; tt < ntl; tt++) {  // one trip unless the source groups tiles
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // the next tile of a multi-tile source (the last tile: its own first
+        // items again, cache hits; branch-free)
+        const int tn = tt + 1 < ntl ? t + 1 : t;
+        const uint4* wpn = wt + (size_t)tn * GQ * 64 + lane;
+        // refill: 1 = item i + D of this tile, 2 = item u of the next tile
         auto step = [&](auto refill_tag, int u, int i) {
             const uint4 wv = wbuf[u];
             if (u % SI == 0) scur = sbuf[u / SI];  // this record serves items i .. i+SI-1
             const typename SR::Rec sv = scur;
-            if constexpr (decltype(refill_tag)::value) {
+            if constexpr (decltype(refill_tag)::value == 1) {
                 if (u % SI == 0) sbuf[u / SI] = *scale_ptr(i + D);
                 wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
+            } else if constexpr (decltype(refill_tag)::value == 2) {
+                if (u % SI == 0) sbuf[u / SI] = *scale_ptr_t(u, tn);
+                wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
             }
             if (i >= nmine) return;  // past this wave's items (wave-uniform: a scalar branch)
             float sj[4];
@@ -748,17 +756,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         const int nbatch = (nmine + D - 1) / D;
         for (int bt = 0; bt + 1 < nbatch; bt++) {
 #pragma unroll
-            for (int u = 0; u < D; u++) step(std::true_type{}, u, bt * D + u);
+            for (int u = 0; u < D; u++) step(std::integral_constant<int, 1>{}, u, bt * D + u);
         }
+        // last batch: a multi-tile source puts the next tile's first items in
+        // flight as each buffer frees, so they stream in during this batch's
+        // MFMAs, the reduction and the epilogue
+        constexpr int LAST = Src::TPW > 1 ? 2 : 0;
         if (nbatch > 0) {
 #pragma unroll
-            for (int u = 0; u < D; u++) step(std::false_type{}, u, (nbatch - 1) * D + u);
-        }
-        if constexpr (Src::TPW > 1) {
-            // the next tile's first items stream in during this tile's reduction;
-            // branch-free: the last tile re-reads its own first items (cache hits)
-            const int tn = tt + 1 < ntl ? t + 1 : t;
-            const uint4* wpn = wt + (size_t)tn * GQ * 64 + lane;
+            for (int u = 0; u < D; u++) step(std::integral_constant<int, LAST>{}, u, (nbatch - 1) * D + u);
+        } else if constexpr (LAST == 2) {
 #pragma unroll
             for (int u = 0; u < D; u++) {
                 if (u % SI == 0) sbuf[u / SI] = *scale_ptr_t(u, tn);
