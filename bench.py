@@ -185,45 +185,55 @@ MOE = dict(d=2048, ff=1408, E=64, S=2, k=6)
 MLA = dict(B=8, H=16, L=4096, dn=128, dr=64, r=512, dv=128)
 
 
-def moe_bench(dev, T, iters):
+def moe_bench(dev, T, iters, layers=2):
     """Config 4 MoE layer forward (router, dispatch, grouped int4 experts,
-    combine) on T tokens.  Algorithmic bytes: every weight byte of the experts
-    the batch routes to (+ shared experts) once, the router, h in, out.
-    `us`: the calls replayed as one HIP graph (the decode loop's launch
-    mode); `stream_launched_us`: the same calls enqueued one by one."""
+    combine) on T tokens.  `layers` independently initialised layers are
+    called in turn, so every call's expert weights were last read a whole
+    layer earlier (2 x 321 MB > 256 MB MALL).  Algorithmic bytes per call:
+    every weight byte of the experts the batch routes to (+ shared experts)
+    once, the router, h in, out (averaged over the layers).  `us`: the calls
+    replayed as one HIP graph (the decode loop's launch mode);
+    `stream_launched_us`: the same calls enqueued one by one."""
     import ctypes
     c = MOE
     L = capi.lib()
-    h = ctypes.c_void_p()
-    capi.check(L.th_moe_create(dev.handle, c["d"], c["ff"], c["E"], c["S"], c["k"], ctypes.byref(h)))
+    hs = []
     try:
-        capi.check(L.th_moe_init_synthetic(h, 4))
+        for i in range(layers):
+            h = ctypes.c_void_p()
+            capi.check(L.th_moe_create(dev.handle, c["d"], c["ff"], c["E"], c["S"], c["k"], ctypes.byref(h)))
+            hs.append(h)
+            capi.check(L.th_moe_init_synthetic(h, 4 + 100 * i))
         x = dev.upload(capi.synth_normal(45, T * c["d"], 1.0, capi.BF16), capi.BF16)
-        out, idx, w = dev.alloc(T * c["d"]), dev.alloc(T * c["k"], capi.I32), dev.alloc(T * c["k"])
-        fwd = lambda: capi.check(L.th_moe_forward(h, x.handle, T, out.handle, idx.handle, w.handle))
-        for _ in range(5):
-            fwd()
+        out = dev.alloc(T * c["d"])
+        idx = [dev.alloc(T * c["k"], capi.I32) for _ in hs]
+        w = [dev.alloc(T * c["k"]) for _ in hs]
+        fwd = lambda i: capi.check(L.th_moe_forward(hs[i % layers], x.handle, T, out.handle, idx[i % layers].handle,
+                                                    w[i % layers].handle))
+        for i in range(2 * layers):
+            fwd(i)
         dev.sync()
         dev.timer_start()
-        for _ in range(iters):
-            fwd()
+        for i in range(iters):
+            fwd(i)
         ms_stream = dev.timer_stop()
-        g = dev.capture(lambda: [fwd() for _ in range(iters)])
+        g = dev.capture(lambda: [fwd(i) for i in range(iters)])
         g.launch()
         dev.timer_start()
         g.launch()
         ms = dev.timer_stop()
         g.free()
-        used = len(np.unique(idx.to_numpy())) + c["S"]
+        used = [len(np.unique(b.to_numpy())) + c["S"] for b in idx]
     finally:
-        L.th_moe_destroy(h)
+        for h in hs:
+            L.th_moe_destroy(h)
     lin = 3 * c["ff"] * c["d"]
-    nbytes = used * (lin // 2 + lin // 32 * 2) + c["E"] * c["d"] * 4 + T * c["d"] * (2 + 4)
+    nbytes = np.mean(used) * (lin // 2 + lin // 32 * 2) + c["E"] * c["d"] * 4 + T * c["d"] * (2 + 4)
     us = ms * 1e3 / iters
     flops = 2 * T * (c["k"] + c["S"]) * lin
     return dict(T=T, us=round(us, 2), experts_read=used, bytes=int(nbytes), gbs=round(nbytes / us / 1e3, 1),
                 frac_hbm=round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4), tflops=round(flops / us / 1e6, 2),
-                stream_launched_us=round(ms_stream * 1e3 / iters, 2))
+                stream_launched_us=round(ms_stream * 1e3 / iters, 2), layers_rotated=layers)
 
 
 def mla_bench(dev, iters, copies=8):
