@@ -54,6 +54,7 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const uint8_t* __restri
     const int TT = MLA_H * R / 16, W = R + dr;
     const int t = min((int)blockIdx.x * 4 + wave, TT - 1);  // surplus waves redo the last tile, store nothing
     const int h = 16 * t / R;
+    const float sc = wsc[16 * t + r];  // loaded now: a load in the store branch would end the kernel with a round trip
     uint4 w[MLA_ABS_CH];
 #pragma unroll
     for (int c = 0; c < MLA_ABS_CH; c++) w[c] = *(const uint4*)(wq + (((size_t)t * nch + min(c, nch - 1)) * 64 + lane) * 16);
@@ -98,7 +99,6 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const uint8_t* __restri
     }
     if ((int)blockIdx.x * 4 + wave < TT) {
         const int row = 16 * t + r, n = row - h * R;
-        const float sc = wsc[row];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int b = 4 * q + j;
@@ -355,6 +355,7 @@ __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const floa
     // this wave's W_UV tile first: it does not depend on the merge
     const int TV = dv / 16, tt = g * 4 + wave;
     const int trow = h * TV + min(tt, TV - 1);  // 16-row tile of the stacked W_UV
+    const float usc = wsc[h * dv + min(tt, TV - 1) * 16 + r];  // loaded with the weights, not in the store branch
     uint4 w[MLA_UP_CH];
 #pragma unroll
     for (int c = 0; c < MLA_UP_CH; c++) w[c] = *(const uint4*)(wq + (((size_t)trow * nch + min(c, nch - 1)) * 64 + lane) * 16);
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const floa
     }
     if (q == 0) {  // D[row 0][col r]: lane (0, r), element 0
         const int n = tt * 16 + r;
-        out[((size_t)b * MLA_H + h) * dv + n] = d[0] * wsc[h * dv + n];
+        out[((size_t)b * MLA_H + h) * dv + n] = d[0] * usc;
     }
 }
 
