@@ -185,7 +185,7 @@ MOE = dict(d=2048, ff=1408, E=64, S=2, k=6)
 MLA = dict(B=8, H=16, L=4096, dn=128, dr=64, r=512, dv=128)
 
 
-def moe_bench(dev, T, iters, layers=2):
+def moe_bench(dev, T, iters, layers=2, graph=True):
     """Config 4 MoE layer forward (router, dispatch, grouped int4 experts,
     combine) on T tokens.  `layers` independently initialised layers are
     called in turn, so every call's expert weights were last read a whole
@@ -217,12 +217,14 @@ def moe_bench(dev, T, iters, layers=2):
         for i in range(iters):
             fwd(i)
         ms_stream = dev.timer_stop()
-        g = dev.capture(lambda: [fwd(i) for i in range(iters)])
-        g.launch()
-        dev.timer_start()
-        g.launch()
-        ms = dev.timer_stop()
-        g.free()
+        ms = ms_stream
+        if graph:
+            g = dev.capture(lambda: [fwd(i) for i in range(iters)])
+            g.launch()
+            dev.timer_start()
+            g.launch()
+            ms = dev.timer_stop()
+            g.free()
         used = [len(np.unique(b.to_numpy())) + c["S"] for b in idx]
     finally:
         for h in hs:
@@ -407,6 +409,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-moe-mla", action="store_true")
+    ap.add_argument("--profile-moe", type=int, default=0,
+                    help="stream-launched MoE forward calls on this many tokens plus a 256 MiB copy, for counter runs")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="counter runs: 240 GEMV launches, then one 256 MiB device copy as the traffic calibration")
     ap.add_argument("--profile-m", type=int, default=0,
@@ -432,6 +436,13 @@ def main():
         return
     if args.profile_gemm:
         print(json.dumps(prefill_bench(dev, 2048, steps=4)))
+        return
+    if args.profile_moe:
+        moe_bench(dev, args.profile_moe, 40, graph=False)
+        a, b = dev.alloc(256 << 20, capi.U8), dev.alloc(256 << 20, capi.U8)
+        capi.check(capi.lib().th_buffer_copy(b.handle, a.handle))
+        dev.sync()
+        print(json.dumps({"profile_moe": args.profile_moe, "calls": 40, "copy_bytes": 256 << 20}))
         return
     if args.profile_gemv:
         gemv_bench(dev, 1, 240, 0, graph=False)  # kernel tracers do not follow graph replays

@@ -729,10 +729,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
         }
         return;
     }
+    // a 16-byte block of the activations (its allocation is 256-byte aligned)
+    const void* xhot = (const void*)((uintptr_t)xin & ~(uintptr_t)15);
     for (int tt = 0; tt < ntl; tt++) {  // one trip unless the source groups tiles
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        // the next tile of a multi-tile source (the last tile: its own first
-        // items again, cache hits; branch-free)
+        // the next tile of a multi-tile source (branch-free: past the last
+        // tile the loads read xhot, below)
         const int tn = tt + 1 < ntl ? t + 1 : t;
         const uint4* wpn = wt + (size_t)tn * GQ * 64 + lane;
         // refill: 1 = item i + D of this tile, 2 = item u of the next tile
@@ -744,8 +746,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
                 if (u % SI == 0) sbuf[u / SI] = *scale_ptr(i + D);
                 wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
             } else if constexpr (decltype(refill_tag)::value == 2) {
-                if (u % SI == 0) sbuf[u / SI] = *scale_ptr_t(u, tn);
-                wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
+                // past the last tile the refill reads the activations (hot
+                // in L2, never used): a re-read of this tile's own items
+                // would stream from HBM again (the weights are loaded
+                // non-temporally)
+                const bool more = tt + 1 < ntl;
+                if (u % SI == 0)
+                    sbuf[u / SI] = more ? *scale_ptr_t(u, tn) : *(const typename SR::Rec*)xhot;
+                wbuf[u] = ldg_stream(more ? wpn + (size_t)item_gq(u) * 64 : (const uint4*)xhot);
             }
             if (i >= nmine) return;  // past this wave's items (wave-uniform: a scalar branch)
             float sj[4];
@@ -766,10 +774,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
             for (int u = 0; u < D; u++) step(std::integral_constant<int, LAST>{}, u, (nbatch - 1) * D + u);
         } else if constexpr (LAST == 2) {
+            const bool more = tt + 1 < ntl;
 #pragma unroll
             for (int u = 0; u < D; u++) {
-                if (u % SI == 0) sbuf[u / SI] = *scale_ptr_t(u, tn);
-                wbuf[u] = ldg_stream(wpn + (size_t)item_gq(u) * 64);
+                if (u % SI == 0) sbuf[u / SI] = more ? *scale_ptr_t(u, tn) : *(const typename SR::Rec*)xhot;
+                wbuf[u] = ldg_stream(more ? wpn + (size_t)item_gq(u) * 64 : (const uint4*)xhot);
             }
         }
         tile_end(t, acc, Src::TPW > 1);
