@@ -52,6 +52,19 @@ def test_mla_small_latent_and_repeat(dev):
         assert max_abs_rel(out, ref) < TOL
 
 
+def test_mla_widest_nope_and_rejects_wider(dev):
+    """qk_nope 256 (four 64-k chunks of W_UK, the absorb's widest) matches the
+    oracle; 260 is rejected with an error, not computed."""
+    out, ref = _run(dev, 3, 150, seed=13, dn=256, dr=32, r=64, dv=32)
+    assert max_abs_rel(out, ref) < TOL
+    qn, qr, cache, wuk, suk, wuv, suv = _case(14, 1, 8, dn=260, dr=32, r=64, dv=32)
+    wk = dev.q8_upload_rowwise(wuk, suk, H * 64, 260)
+    wv = dev.q8_upload_rowwise(wuv, suv, H * 32, 64)
+    with pytest.raises(capi.TangHipError):
+        dev.mla_decode(dev.upload(qn), dev.upload(qr), dev.upload(cache, capi.BF16), 1, H, 8, 260, 32, 64, 32, wk, wv,
+                       0.1)
+
+
 def test_mla_graph_replay_matches_eager(dev):
     """th_capture_begin/end around two calls, replayed three times with eager
     calls and synchronisations between the replays: every replay gives the
