@@ -446,12 +446,15 @@ class HipComputeDevice:
         """Record the library calls fn() makes on this device's stream into a
         Graph (th_capture_begin / th_capture_end)."""
         check(lib().th_capture_begin(self.handle))
+        h = ctypes.c_void_p()
         try:
             fn()
-        finally:
-            h = ctypes.c_void_p()
-            rc = lib().th_capture_end(self.handle, ctypes.byref(h))
-        check(rc)
+        except BaseException:
+            # end the capture (the stream must leave capture mode) and drop its graph
+            if lib().th_capture_end(self.handle, ctypes.byref(h)) == 0 and h:
+                lib().th_graph_destroy(h)
+            raise
+        check(lib().th_capture_end(self.handle, ctypes.byref(h)))
         return Graph(h)
 
     # -- quantized weights
