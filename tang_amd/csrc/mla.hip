@@ -333,9 +333,10 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
 // Split merge fused with the W_UV up-projection: workgroup (head h,
 // sequence b, row group g).  o_lat[b][h] = sum_s w_s acc_s / sum_s w_s l_s
 // (split order, w_s = exp(m_s - max m)) is built in LDS, then each wave
-// takes one 16-row tile of the head's W_UV rows on MFMA, as the absorb:
-// A = o_lat (row 0; hi + lo bf16), B = the tile's int8 weights as bf16,
-// MFMA k index 8q + e of step (c, hh) = k c*64 + 16q + 8hh + e.  The W_UV
+// takes one 16-row tile of the head's W_UV rows on v_mfma_f32_16x16x32_f16:
+// A = o_lat (row 0; scaled by a power of two into f16 range, as hi + lo f16
+// parts), B = the tile's int8 weights as f16 (exact), MFMA k index 8q + e of
+// step (c, hh) = k c*64 + 16q + 8hh + e.  The W_UV
 // and record loads are all issued at the start.  r <= 512, dv <= 128,
 // n_splits <= 64.
 constexpr int MLA_UP_THREADS = 256;
@@ -345,9 +346,10 @@ __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const floa
                                                                      int R, const uint8_t* __restrict__ wq,
                                                                      const float* __restrict__ wsc, int dv, int nch,
                                                                      float* __restrict__ out) {
-    __shared__ __align__(16) float olat[512];
+    __shared__ __align__(16) uint16_t olh[2][512];  // o_lat * 2^-oe as f16 hi, lo parts
     __shared__ float wts[64];
     __shared__ float Lsh;
+    __shared__ float omax4[4];
     const int h = blockIdx.x, b = blockIdx.y, g = blockIdx.z, tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), q = lane >> 4, r = lane & 15;
     const float* recs = part + (size_t)b * n_splits * MLA_H * (R + 2);
@@ -394,43 +396,55 @@ __global__ __launch_bounds__(MLA_UP_THREADS) void mla_merge_up_kernel(const floa
 #pragma unroll
             for (int j = 0; j < DPT; j++) a[j] += s0 + i < n_splits ? v[i][j] * wts[s0 + i] : 0.0f;
     }
+    // o_lat in f16 range: scaled by 2^-oe so that its largest magnitude lies
+    // in [2^12, 2^13), as hi + lo f16 parts (the result is scaled back exactly)
+    float o[DPT], om = 0.0f;
 #pragma unroll
-    for (int j = 0; j < DPT; j++) olat[tid + 256 * j] = tid + 256 * j < R ? a[j] / Lsh : 0.0f;
+    for (int j = 0; j < DPT; j++) {
+        o[j] = tid + 256 * j < R ? a[j] / Lsh : 0.0f;
+        om = fmaxf(om, fabsf(o[j]));
+    }
+    const int oe = range_exp(block_absmax256(om, omax4), XPREP_TOP);
+#pragma unroll
+    for (int j = 0; j < DPT; j++) {
+        const float os = __builtin_amdgcn_ldexpf(o[j], -oe);
+        const _Float16 hi = (_Float16)os;
+        olh[0][tid + 256 * j] = __builtin_bit_cast(uint16_t, hi);
+        olh[1][tid + 256 * j] = __builtin_bit_cast(uint16_t, (_Float16)(os - (float)hi));
+    }
     __syncthreads();
     if (tt >= TV) return;  // wave-uniform: no barrier follows
+    // A = o_lat (row 0; hi and lo f16 parts, the other rows zero), B = the
+    // tile's int8 weights as f16, exact: bytes ^ 0x80 spliced under an f16
+    // exponent of 2^10 give 1024 + w + 128, less 1152
     float4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+    const half2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
     for (int c = 0; c < MLA_UP_CH; c++) {
         if (c >= nch) break;
-        const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+        const uint32_t ww[4] = {w[c].x ^ 0x80808080u, w[c].y ^ 0x80808080u, w[c].z ^ 0x80808080u, w[c].w ^ 0x80808080u};
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
-            // o_lat as A row 0 (the other rows zero): k = c*64 + 16q + 8hh + e
-            const float4 o0 = *(const float4*)&olat[min(c * 64 + 16 * q + 8 * hh, 504)];
-            const float4 o1 = *(const float4*)&olat[min(c * 64 + 16 * q + 8 * hh + 4, 508)];
-            const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
-            uint32_t bw[4], ah[4], al[4];
+            uint32_t bw[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t word = ww[2 * hh + (e >> 1)];
-                const int sh = 16 * (e & 1);
-                const float w0 = (float)(int8_t)(word >> sh), w1 = (float)(int8_t)(word >> (sh + 8));
-                bw[e] = (__float_as_uint(w0) >> 16) | (__float_as_uint(w1) & 0xFFFF0000u);  // exact: |w| <= 127
-                const float x0 = r == 0 ? ov[2 * e] : 0.0f, x1 = r == 0 ? ov[2 * e + 1] : 0.0f;
-                const uint32_t h0 = f32_to_bf16_bits(x0), h1 = f32_to_bf16_bits(x1);
-                ah[e] = h0 | (h1 << 16);
-                al[e] = f32_to_bf16_bits(x0 - bf16_bits_to_f32(h0)) | (f32_to_bf16_bits(x1 - bf16_bits_to_f32(h1)) << 16);
+            for (int e = 0; e < 2; e++) {
+                const uint32_t word = ww[2 * hh + e];
+                const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, word, 0x04010400u);
+                const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, word, 0x04030402u);
+                bw[2 * e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, p0) + off);
+                bw[2 * e + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, p1) + off);
             }
-            const bf16x8_t B8 = __builtin_bit_cast(bf16x8_t, make_uint4(bw[0], bw[1], bw[2], bw[3]));
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(ah[0], ah[1], ah[2], ah[3])),
-                                                        B8, d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(al[0], al[1], al[2], al[3])),
-                                                        B8, d, 0, 0, 0);
+            const int k0 = min(c * 64 + 16 * q + 8 * hh, 504);  // k >= R: zero weight (padding)
+            const uint4 ah = *(const uint4*)&olh[0][k0], al = *(const uint4*)&olh[1][k0];
+            const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+            const half8_t B8 = __builtin_bit_cast(half8_t, make_uint4(bw[0], bw[1], bw[2], bw[3]));
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r == 0 ? ah : z), B8, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, r == 0 ? al : z), B8, d, 0, 0, 0);
         }
     }
     if (q == 0) {  // D[row 0][col r]: lane (0, r), element 0
         const int n = tt * 16 + r;
-        out[((size_t)b * MLA_H + h) * dv + n] = d[0] * usc;
+        out[((size_t)b * MLA_H + h) * dv + n] = __builtin_amdgcn_ldexpf(d[0], oe) * usc;
     }
 }
 

@@ -52,6 +52,24 @@ def test_mla_small_latent_and_repeat(dev):
         assert max_abs_rel(out, ref) < TOL
 
 
+@pytest.mark.parametrize("scale_exp", [18, -18])
+def test_mla_cache_far_from_unit_range(dev, scale_exp):
+    """A latent cache scaled by 2^18 (o_lat far above f16's 65504) or 2^-18
+    (far below f16's normal range): the up-projection's f16 operands are
+    scaled by a power of two per head, so the result still matches."""
+    B, L = 2, 300
+    qn, qr, cache, wuk, suk, wuv, suv = _case(21, B, L)
+    c = (cache.astype(np.uint32) << 16).view(np.float32) * np.float32(2.0 ** scale_exp)
+    cache = (c.view(np.uint32) >> 16).astype(np.uint16)  # exact: a power-of-two scale of bf16 values
+    scale = 1.0 / np.sqrt(DN + DR) * 2.0 ** (-scale_exp)  # scores keep their spread
+    ref = oracle.mla_decode(qn, qr, cache, B, H, L, DN, DR, R, DV, wuk, suk, wuv, suv, scale)
+    wk = dev.q8_upload_rowwise(wuk, suk, H * R, DN)
+    wv = dev.q8_upload_rowwise(wuv, suv, H * DV, R)
+    out = dev.mla_decode(dev.upload(qn), dev.upload(qr), dev.upload(cache, capi.BF16), B, H, L, DN, DR, R, DV,
+                         wk, wv, scale).to_numpy()
+    assert np.isfinite(out).all() and max_abs_rel(out, ref) < TOL
+
+
 def test_mla_widest_nope_and_rejects_wider(dev):
     """qk_nope 256 (four 64-k chunks of W_UK, the absorb's widest) matches the
     oracle; 260 is rejected with an error, not computed."""
