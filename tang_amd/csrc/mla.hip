@@ -35,6 +35,19 @@ constexpr int MLA_H = 16;       // heads per MFMA row block (config 5: 16)
 constexpr int MLA_CHUNK = 64;   // positions staged per pass
 constexpr int MLA_SPLIT = 128;  // positions per workgroup
 
+typedef __bf16 bf16x2_pk_t __attribute__((ext_vector_type(2)));
+// Two f32 values as a bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32;
+// the same bits as f32_to_bf16_bits for finite values).
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    const bf16x2_pk_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+// hi and lo bf16 pairs of (a, b): hi + lo carries 16 significant bits of each
+__device__ __forceinline__ void bf16_pair_hilo(float a, float b, uint32_t& hi, uint32_t& lo) {
+    hi = bf16_pair(a, b);
+    lo = bf16_pair(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
+}
+
 // Absorb on MFMA: q_lat[b][h][n] = scale[h*R+n] * sum_k W_UK[h*R+n][k] x[b][h][k]
 // for every sequence b at once.  One wave per 16-row tile of the stacked
 // W_UK (q8 tiles: 16 rows x 64 k, lane q*16+r holding k 16q..16q+15 of row
@@ -86,9 +99,7 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const uint8_t* __restri
                 const bool live = r < B;
                 const float x0 = live && k0 < dn ? ((e & 1) ? xf.z : xf.x) : 0.0f;
                 const float x1 = live && k0 + 1 < dn ? ((e & 1) ? xf.w : xf.y) : 0.0f;
-                const uint32_t h0 = f32_to_bf16_bits(x0), h1 = f32_to_bf16_bits(x1);
-                ah[e] = h0 | (h1 << 16);
-                al[e] = f32_to_bf16_bits(x0 - bf16_bits_to_f32(h0)) | (f32_to_bf16_bits(x1 - bf16_bits_to_f32(h1)) << 16);
+                bf16_pair_hilo(x0, x1, ah[e], al[e]);
             }
             const bf16x8_t B8 = __builtin_bit_cast(bf16x8_t, make_uint4(bw[0], bw[1], bw[2], bw[3]));
             d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, make_uint4(ah[0], ah[1], ah[2], ah[3])),
@@ -268,13 +279,7 @@ __global__ __launch_bounds__(MLA_THREADS) void mla_attn_kernel(const uint16_t* _
             const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
             uint32_t h2[4], l2[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t ha = f32_to_bf16_bits(pv[2 * e]), hb = f32_to_bf16_bits(pv[2 * e + 1]);
-                const uint32_t la = f32_to_bf16_bits(pv[2 * e] - bf16_bits_to_f32(ha));
-                const uint32_t lb = f32_to_bf16_bits(pv[2 * e + 1] - bf16_bits_to_f32(hb));
-                h2[e] = ha | (hb << 16);
-                l2[e] = la | (lb << 16);
-            }
+            for (int e = 0; e < 4; e++) bf16_pair_hilo(pv[2 * e], pv[2 * e + 1], h2[e], l2[e]);
             ahi[kk] = make_uint4(h2[0], h2[1], h2[2], h2[3]);
             alo[kk] = make_uint4(l2[0], l2[1], l2[2], l2[3]);
         }
