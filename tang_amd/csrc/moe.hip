@@ -213,6 +213,19 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float* __restrict__
 // and keeps the indices in LDS for the slot passes: one launch instead of two
 // for decode-sized batches.
 constexpr int MOE_FUSED_ENTRIES = 1024;
+// Inclusive prefix sum over the 64 lanes with DPP: row_shr 1, 2, 4, 8
+// within each row of 16 (lanes without a source add 0), then row_bcast:15
+// and row_bcast:31 carry each row's total into the rows above it.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+    return x;
+}
+
 template <int PL>
 __global__ __launch_bounds__(1024) void moe_dispatch_kernel(const float* __restrict__ logits, int32_t* __restrict__ topk_idx_out,
                                                             float* __restrict__ topk_w_out,
@@ -272,12 +285,7 @@ __global__ __launch_bounds__(1024) void moe_dispatch_kernel(const float* __restr
         __shared__ int wsum[2][16];
         const int tv = tid < NE ? tot[tid] : 0;
         const int wv = (tv + rows - 1) / rows;
-        int a = tv, b = wv;  // inclusive scans within the wave
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int ta = __shfl_up(a, o, 64), tb = __shfl_up(b, o, 64);
-            if (lane >= o) { a += ta; b += tb; }
-        }
+        const int a = wave_incl_scan(tv), b = wave_incl_scan(wv);  // inclusive scans within the wave
         if (lane == 63) { wsum[0][wave] = a; wsum[1][wave] = b; }
         __syncthreads();
         int oa = 0, ob = 0;
