@@ -41,10 +41,11 @@ CFG7B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=32, head_dim=128,
              max_seq=2176, eps=1e-5, rope_theta=1e4)
 
 
-def gemv_bench(dev, m, steps, warmup, graph=True):
+def gemv_bench(dev, m, steps, warmup, graph="aql"):
     """Elapsed ms of `steps` config-2 linears over N_COPIES weight copies;
-    graph=True replays them as one HIP graph (the decode engine's launch
-    mode), False launches each on the stream."""
+    graph="aql" replays them as one sequence on the library's AQL queue (the
+    decode engine's launch mode: no release fences between the launches),
+    True as one HIP graph, False launches each on the stream."""
     nib, sc16 = capi.synth_q4(2, N, K)
     ws = [dev.q4_upload_packed(nib, sc16, N, K, capi.F16) for _ in range(N_COPIES)]
     x = dev.upload(capi.synth_normal(3, m * K, 1.0, capi.BF16), capi.BF16)
@@ -456,6 +457,8 @@ def main():
     gbs = GEMV_BYTES[1] / us / 1e3
     ms_stream = gemv_bench(dev, 1, args.steps, 0, graph=False)
     us_stream = ms_stream * 1e3 / args.steps
+    ms_graph = gemv_bench(dev, 1, args.steps, 0, graph=True)
+    us_graph = ms_graph * 1e3 / args.steps
     extra = {}
     for m in (4, 8, 16):
         msm = gemv_bench(dev, m, max(args.steps // 4, 48), 24)
@@ -484,12 +487,14 @@ def main():
         "dtype": "int4 weights x bf16 activations, fp32 accumulate",
         "data": "synthetic (seeded xoshiro256**; int4 ~U[-8,7], f16 scales ~U[0.002,0.01], x bf16 ~N(0,1))",
         "config": {"workload": "q4 g32 GEMV 11008x4096, M=1, bf16 activations (BASELINE config 2), "
-                               "%d rotating weight copies (305 MB > 256 MB MALL), launches replayed as one HIP graph"
+                               "%d rotating weight copies (305 MB > 256 MB MALL), launches replayed as one sequence on the "
+                               "library's AQL queue (no release fences between launches; device clock stamps)"
                                % N_COPIES,
                    "timed_launches": args.steps,
-                   "before_timing": "the graph replayed once, then one launch per weight copy in copy order, so "
+                   "before_timing": "the sequence replayed once, then one launch per weight copy in copy order, so "
                                     "every timed read of a copy is %d launches after its previous one" % N_COPIES,
                    "stream_launched": dict(us=round(us_stream, 3), gbs=round(GEMV_BYTES[1] / us_stream / 1e3, 1)),
+                   "hip_graph": dict(us=round(us_graph, 3), gbs=round(GEMV_BYTES[1] / us_graph / 1e3, 1)),
                    "M_sweep": extra},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_BYTES,

@@ -187,8 +187,11 @@ int th_gemm_q4_noalloc(th_device* dev, const th_buffer* x, size_t m, const th_qw
  * th_gemm_q4 / th_gemv_q8 (by the weights' bit width) on x -> y, cycling
  * through the n_w weights (all of one shape) so the streamed bytes exceed the
  * last-level cache, and return the elapsed milliseconds between HIP events
- * recorded on the device stream around them.  use_graph != 0 captures the
- * calls into one HIP graph first and times its replay.  Launch i reads weight
+ * recorded on the device stream around them.  use_graph == 1 captures the
+ * calls into one HIP graph first and times its replay; use_graph == 2 records
+ * them as one sequence on the library's own AQL queue (no release fences
+ * between the q4 GEMV launches, whose outputs are stored write-through) and
+ * times its replay between device clock stamps.  Launch i reads weight
  * ws[i % n_w], and the untimed warm-up ends with one pass over ws[0..n_w) in
  * that order, so every timed launch's weights were last read n_w launches
  * earlier, for any iters. */
@@ -311,8 +314,9 @@ int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, in
 int th_llama_step_device(th_llama* m, size_t pos);
 int th_llama_set_token(th_llama* m, int32_t token);
 /* Benchmark helper: run n_steps greedy steps from (token, pos) as in
- * th_llama_generate and return the milliseconds between HIP events recorded
- * on the device stream around the step launches. */
+ * th_llama_generate and return the milliseconds between device clock stamps
+ * around the step replays on the library's AQL queue (between HIP events
+ * around the graph launches when TANG_HIP_DISPATCH=graph). */
 int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, float* ms);
 
 /* Prefill: the prompt tokens[0..n) at positions pos..pos+n-1 run through

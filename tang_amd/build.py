@@ -61,7 +61,7 @@ def build(jobs=None, verbose=True):
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fopenmp", "-o", tmp] + objs + ["-lhiprtc"]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fopenmp", "-o", tmp] + objs + ["-lhiprtc", "-lhsa-runtime64", "-ldl"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed: %s\n%s" % (r.stdout, r.stderr))

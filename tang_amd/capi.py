@@ -496,11 +496,14 @@ class HipComputeDevice:
         return y
 
     def bench_linear(self, x, m, weights, y, iters, use_graph=False):
-        """Elapsed ms of `iters` quantized linears cycling through `weights`."""
+        """Elapsed ms of `iters` quantized linears cycling through `weights`:
+        launched one by one (use_graph False), replayed as a HIP graph (True)
+        or as a sequence on the library's AQL queue ("aql")."""
         arr = (ctypes.c_void_p * len(weights))(*[w.handle.value for w in weights])
         ms = ctypes.c_float()
+        mode = 2 if use_graph == "aql" else (1 if use_graph else 0)
         check(lib().th_bench_linear(self.handle, x.handle, m, arr, len(weights), y.handle, iters,
-                                    1 if use_graph else 0, ctypes.byref(ms)))
+                                    mode, ctypes.byref(ms)))
         return ms.value
 
     # -- decode ops

@@ -54,11 +54,11 @@ void launch_kv_attention(const float* q, const void* kc, const void* vc, bool f1
     if (!tuned) {
         TH_REQUIRE(head_dim <= 512, "head_dim above 512 is not supported");
         if (f16)
-            hipLaunchKernelGGL(attn_generic_kernel<_Float16>, dim3((unsigned)n_heads, (unsigned)q_len), dim3(64), 0, s, q,
+            TH_LAUNCH(attn_generic_kernel<_Float16>, dim3((unsigned)n_heads, (unsigned)q_len), dim3(64), 0, s, q,
                                (const _Float16*)kc, (const _Float16*)vc, (int)cache_start, (int)n_heads,
                                (int)n_kv_heads, (int)head_dim, out);
         else
-            hipLaunchKernelGGL(attn_generic_kernel<float>, dim3((unsigned)n_heads, (unsigned)q_len), dim3(64), 0, s, q,
+            TH_LAUNCH(attn_generic_kernel<float>, dim3((unsigned)n_heads, (unsigned)q_len), dim3(64), 0, s, q,
                                (const float*)kc, (const float*)vc, (int)cache_start, (int)n_heads, (int)n_kv_heads,
                                (int)head_dim, out);
         TH_LAUNCH_CHECK();

@@ -376,10 +376,10 @@ inline void launch_attn_prefill(const float* q, int ldq, const _Float16* kc, con
     TH_REQUIRE(n >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0, "prefill attention: bad shape");
     const dim3 grid((unsigned)ceil_div((size_t)n, (size_t)64), (unsigned)n_heads);
     switch (head_dim * 2 + (xp ? 1 : 0)) {
-        case 128: hipLaunchKernelGGL((attn_prefill_kernel<64, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
-        case 129: hipLaunchKernelGGL((attn_prefill_kernel<64, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
-        case 256: hipLaunchKernelGGL((attn_prefill_kernel<128, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
-        case 257: hipLaunchKernelGGL((attn_prefill_kernel<128, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
+        case 128: TH_LAUNCH((attn_prefill_kernel<64, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
+        case 129: TH_LAUNCH((attn_prefill_kernel<64, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
+        case 256: TH_LAUNCH((attn_prefill_kernel<128, false>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
+        case 257: TH_LAUNCH((attn_prefill_kernel<128, true>), grid, dim3(256), 0, s, q, ldq, kc, vc, n_heads, n_kv_heads, pos0, n, out, ldo, xexp); break;
         default: throw Error(TH_ERR_INVALID, "prefill attention: head_dim must be 64 or 128");
     }
     TH_LAUNCH_CHECK();
@@ -539,8 +539,8 @@ __global__ __launch_bounds__(NT) void attn_decode_kernel(const float* __restrict
         }
         const float v = A * (1.0f / L);
         const size_t oi = (size_t)h * D + d;
-        if (OUT_BF16) ((uint16_t*)out)[oi] = f32_to_bf16_rne(v);
-        else ((float*)out)[oi] = v;
+        if (OUT_BF16) st_coherent(&((uint16_t*)out)[oi], f32_to_bf16_rne(v));
+        else st_coherent(&((float*)out)[oi], v);
     }
 }
 
@@ -562,11 +562,11 @@ inline void launch_attn_split_d(const float* q, const void* kc, const void* vc, 
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     }
     if (f16)
-        hipLaunchKernelGGL((attn_split_kernel<D, _Float16, OUT_BF16>), grid, dim3(256), lds, s, q, (const _Float16*)kc,
+        TH_LAUNCH((attn_split_kernel<D, _Float16, OUT_BF16>), grid, dim3(256), lds, s, q, (const _Float16*)kc,
                            (const _Float16*)vc, cache_start, n_heads, n_kv_heads, subs, n_splits, part, counters, out,
                            cache_start_dev);
     else
-        hipLaunchKernelGGL((attn_split_kernel<D, float, OUT_BF16>), grid, dim3(256), lds, s, q, (const float*)kc,
+        TH_LAUNCH((attn_split_kernel<D, float, OUT_BF16>), grid, dim3(256), lds, s, q, (const float*)kc,
                            (const float*)vc, cache_start, n_heads, n_kv_heads, subs, n_splits, part, counters, out,
                            cache_start_dev);
     TH_LAUNCH_CHECK();
@@ -597,9 +597,9 @@ inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float1
     const dim3 grid((unsigned)n_heads, 1, (unsigned)n_splits);
     const size_t lds = 0;
     switch (head_dim) {
-        case 64: hipLaunchKernelGGL((attn_decode_kernel<64, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 128: hipLaunchKernelGGL((attn_decode_kernel<128, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 256: hipLaunchKernelGGL((attn_decode_kernel<256, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 64: TH_LAUNCH((attn_decode_kernel<64, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 128: TH_LAUNCH((attn_decode_kernel<128, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 256: TH_LAUNCH((attn_decode_kernel<256, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
         default: throw Error(TH_ERR_INVALID, "launch_attn_decode: unsupported head_dim");
     }
     TH_LAUNCH_CHECK();

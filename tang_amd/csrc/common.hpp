@@ -7,6 +7,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 
 #include "../../include/tang_hip.h"
 
@@ -36,6 +37,47 @@ void set_last_error(const std::string& msg);
 
 // Check the launch that was just enqueued.
 #define TH_LAUNCH_CHECK() TH_HIP(hipGetLastError())
+
+// Kernel launches go through launch_kernel: a HIP launch on the stream, or,
+// while this thread records an AQL sequence (aql.cpp), a packet of that
+// sequence with the arguments laid out as the kernel's kernarg segment
+// (each parameter at its natural alignment, in order).
+struct AqlSeq;
+AqlSeq* aql_recording();
+void aql_record_launch(AqlSeq* seq, const void* kernel, dim3 grid, dim3 block, size_t shmem, const void* args,
+                       size_t bytes);
+
+constexpr size_t KERNARG_MAX = 1024;
+
+template <typename P>
+inline void kernarg_put(char* buf, size_t& off, const P& v) {
+    off = (off + alignof(P) - 1) / alignof(P) * alignof(P);
+    if (off + sizeof(P) > KERNARG_MAX) throw Error(TH_ERR_INVALID, "kernel arguments exceed the kernarg buffer");
+    std::memcpy(buf + off, &v, sizeof(P));
+    off += sizeof(P);
+}
+
+template <typename... P, typename... A>
+inline void launch_kernel(void (*kernel)(P...), dim3 grid, dim3 block, size_t shmem, hipStream_t stream,
+                          A&&... args) {
+    static_assert(sizeof...(P) == sizeof...(A), "argument count does not match the kernel");
+    if (AqlSeq* seq = aql_recording()) {
+        alignas(16) char buf[KERNARG_MAX];
+        size_t off = 0;
+        (kernarg_put<P>(buf, off, static_cast<P>(args)), ...);
+        aql_record_launch(seq, (const void*)kernel, grid, block, shmem, buf, off);
+        return;
+    }
+    std::tuple<P...> vals(static_cast<P>(args)...);
+    void* ptrs[sizeof...(P) + 1];
+    std::apply([&](auto&... v) {
+        size_t i = 0;
+        ((ptrs[i++] = (void*)&v), ...);
+    }, vals);
+    (void)hipLaunchKernel((const void*)kernel, grid, block, ptrs, shmem, stream);
+}
+
+#define TH_LAUNCH(...) ::th::launch_kernel(__VA_ARGS__)
 
 inline size_t dtype_size(th_dtype t) {
     switch (t) {
@@ -72,6 +114,12 @@ inline uint16_t f32_to_f16_host(float v) { return __builtin_bit_cast(uint16_t, (
 // Library objects behind the opaque C handles.
 // ---------------------------------------------------------------------------
 
+namespace th {
+struct AqlDev;
+void aql_wait(th_device* d);
+void aql_release(th_device* d);
+}  // namespace th
+
 struct th_device {
     int ordinal = 0;
     hipStream_t stream = nullptr;
@@ -86,6 +134,7 @@ struct th_device {
     size_t n_counters = 0;
     int live = 0;          // buffers, weights and engines that hold this device
     bool closed = false;   // th_device_destroy ran; the struct waits for live == 0
+    th::AqlDev* aql = nullptr;  // HSA queue for recorded sequences (created on first use)
 };
 
 // Objects holding a th_device keep the struct alive: th_device_destroy
@@ -99,7 +148,12 @@ inline void device_release(th_device* d) {
 // Drain the device's stream before freeing memory it may still use (nothing
 // is in flight once the device is closed).
 inline void device_drain(th_device* d) {
-    if (!d->closed) (void)hipStreamSynchronize(d->stream);
+    if (d->closed) return;
+    try {
+        th::aql_wait(d);
+    } catch (...) {
+    }
+    (void)hipStreamSynchronize(d->stream);
 }
 
 // A captured sequence of library calls (th_capture_begin / th_capture_end).

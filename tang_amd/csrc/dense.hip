@@ -129,7 +129,7 @@ static void matmul_launch2(const th_buffer* a, const th_buffer* b, th_buffer* c,
     const dim3 grid((unsigned)ceil_div(n, MM_T), (unsigned)ceil_div(m, MM_T));
     const bool abf = a->dtype == TH_BF16, bbf = b->dtype == TH_BF16;
 #define TH_MM(AB, BB)                                                                                          \
-    hipLaunchKernelGGL((matmul_kernel<TA, TB, AB, BB>), grid, dim3(256), 0, s, a->ptr, b->ptr, (float*)c->ptr, \
+    TH_LAUNCH((matmul_kernel<TA, TB, AB, BB>), grid, dim3(256), 0, s, a->ptr, b->ptr, (float*)c->ptr, \
                        (int)m, (int)n, (int)k, acc)
     if (abf && bbf) TH_MM(true, true);
     else if (abf) TH_MM(true, false);
@@ -232,7 +232,7 @@ int th_transpose_2d(th_device* dev, const th_buffer* in, size_t rows, size_t col
     TH_REQUIRE(rows < (1u << 31) && cols < (1u << 31), "transpose: dimension too large");
     if (rows == 0 || cols == 0) return TH_OK;
     TH_REQUIRE(ceil_div(rows, 32) < 65536, "transpose: more than 2^21 rows");
-    hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)ceil_div(cols, 32), (unsigned)ceil_div(rows, 32)), dim3(256), 0,
+    TH_LAUNCH(transpose_kernel, dim3((unsigned)ceil_div(cols, 32), (unsigned)ceil_div(rows, 32)), dim3(256), 0,
                        dev->stream, (const float*)in->ptr, (float*)out->ptr, (int)rows, (int)cols);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -250,7 +250,7 @@ int th_reduce_sum(th_device* dev, const th_buffer* in, const size_t* shape, size
     require_len(in, TH_F32, outer * len * inner, "in");
     require_len(out, TH_F32, outer * inner, "out");
     if (outer * inner == 0) return TH_OK;
-    hipLaunchKernelGGL(reduce_sum_kernel, dim3(grid_of(outer * inner)), dim3(256), 0, dev->stream,
+    TH_LAUNCH(reduce_sum_kernel, dim3(grid_of(outer * inner)), dim3(256), 0, dev->stream,
                        (const float*)in->ptr, (float*)out->ptr, outer, len, inner, accumulate);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -265,7 +265,7 @@ int th_bias_add(th_device* dev, const th_buffer* matrix, const th_buffer* bias, 
     require_len(bias, TH_F32, dim, "bias");
     require_len(out, TH_F32, numel, "out");
     if (numel == 0) return TH_OK;
-    hipLaunchKernelGGL(bias_add_kernel, dim3(grid_of(numel)), dim3(256), 0, dev->stream, (const float*)matrix->ptr,
+    TH_LAUNCH(bias_add_kernel, dim3(grid_of(numel)), dim3(256), 0, dev->stream, (const float*)matrix->ptr,
                        (const float*)bias->ptr, (float*)out->ptr, numel, dim);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -277,7 +277,7 @@ int th_add_assign(th_device* dev, th_buffer* dst, const th_buffer* src) {
     TH_REQUIRE(dst->dtype == TH_F32 && src->dtype == TH_F32, "add_assign: f32 buffers");
     TH_REQUIRE(dst->n == src->n, "add_assign: lengths differ");  // cpu.rs:651 asserts equal lengths
     if (dst->n == 0) return TH_OK;
-    hipLaunchKernelGGL(add_assign_kernel, dim3(grid_of(dst->n)), dim3(256), 0, dev->stream, (float*)dst->ptr,
+    TH_LAUNCH(add_assign_kernel, dim3(grid_of(dst->n)), dim3(256), 0, dev->stream, (float*)dst->ptr,
                        (const float*)src->ptr, dst->n);
     TH_LAUNCH_CHECK();
     TH_API_END

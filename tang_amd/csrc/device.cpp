@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "capi_util.hpp"
+#include "aql.hpp"
 #include "qlinear.hpp"
 
 namespace th {
@@ -265,8 +266,9 @@ int th_device_destroy(th_device* d) {
     TH_API_BEGIN
     if (!d) return TH_OK;
     (void)hipSetDevice(d->ordinal);
-    (void)hipStreamSynchronize(d->stream);
     TH_REQUIRE(!d->closed, "device already destroyed");
+    th::aql_release(d);
+    (void)hipStreamSynchronize(d->stream);
     if (d->scratch) (void)hipFree(d->scratch);
     if (d->scratch_x) (void)hipFree(d->scratch_x);
     if (d->counters) (void)hipFree(d->counters);
@@ -284,7 +286,7 @@ int th_device_destroy(th_device* d) {
 int th_sync(th_device* d) {
     TH_API_BEGIN
     TH_REQUIRE(d, "null device");
-    TH_HIP(hipStreamSynchronize(d->stream));
+    th::device_sync(d);
     TH_API_END
 }
 

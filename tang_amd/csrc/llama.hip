@@ -22,6 +22,7 @@
 #include <cstdlib>
 #include <vector>
 
+#include "aql.hpp"
 #include "attention.hpp"
 #include "capi_util.hpp"
 #include "ops.hpp"
@@ -87,9 +88,9 @@ struct EpiQKV : EpiNoFinish {
                 out = x0 * s + x1 * c;
             }
         }
-        if (n < qd) q[n] = out;
-        else if (n < qd + kvd) kc[(size_t)pos * kvd + (n - qd)] = (_Float16)out;
-        else vc[(size_t)pos * kvd + (n - qd - kvd)] = (_Float16)out;
+        if (n < qd) st_coherent(&q[n], out);
+        else if (n < qd + kvd) st_coherent(&kc[(size_t)pos * kvd + (n - qd)], (_Float16)out);
+        else st_coherent(&vc[(size_t)pos * kvd + (n - qd - kvd)], (_Float16)out);
     }
 };
 
@@ -100,7 +101,7 @@ struct EpiAddToSsq {
     float* x; float* ssq;
     __device__ __forceinline__ void operator()(int, int n, float v, const float*, float* aux) const {
         const float xn = x[n] + v;
-        x[n] = xn;
+        st_coherent(&x[n], xn);
         aux[n & 15] = xn;
     }
     __device__ __forceinline__ void finish(int t, int, const float* aux, int tid) const {
@@ -108,7 +109,7 @@ struct EpiAddToSsq {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; i++) s += aux[i] * aux[i];
-            ssq[t] = s;
+            st_coherent(&ssq[t], s);
         }
     }
 };
@@ -119,7 +120,7 @@ struct EpiSwiGLU : EpiNoFinish {
     uint16_t* out;
     __device__ __forceinline__ void operator()(int, int n, float v, const float* tile, float*) const {
         const int rr = n & 15;
-        if (rr < 8) out[(n >> 4) * 8 + rr] = f32_to_bf16_rne(swiglu_f64(v, tile[rr + 8]));
+        if (rr < 8) st_coherent(&out[(n >> 4) * 8 + rr], f32_to_bf16_rne(swiglu_f64(v, tile[rr + 8])));
     }
 };
 
@@ -131,7 +132,7 @@ struct EpiTileMax {
     static constexpr bool HAS_FINISH = true;
     float* logits; float* part_v; int* part_i; int vocab;
     __device__ __forceinline__ void operator()(int, int n, float v, const float*, float* aux) const {
-        logits[n] = v;
+        st_coherent(&logits[n], v);
         aux[n & 15] = v;
     }
     __device__ __forceinline__ void finish(int t, int, const float* aux, int tid) const {
@@ -141,8 +142,8 @@ struct EpiTileMax {
             int bi = t * 16;
             for (int i = 0; i < cnt; i++)
                 if (aux[i] > bv) { bv = aux[i]; bi = t * 16 + i; }
-            part_v[t] = bv;
-            part_i[t] = bi;
+            st_coherent(&part_v[t], bv);
+            st_coherent(&part_i[t], bi);
         }
     }
 };
@@ -179,10 +180,11 @@ __global__ __launch_bounds__(1024) void llama_argmax_embed_kernel(const float* _
         for (int w = 1; w < 16; w++)
             if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) { bv = wv[w]; bi = wi[w]; }
         const int tok = bi == 0x7fffffff ? 0 : bi;
-        history[st->step] = tok;
-        st->token = tok;
-        st->step += 1;
-        st->pos += 1;
+        const int step = st->step, pos = st->pos;
+        st_coherent(&history[step], tok);
+        st_coherent(&st->token, tok);
+        st_coherent(&st->step, step + 1);
+        st_coherent(&st->pos, pos + 1);
         s_tok = tok;
     }
     __syncthreads();
@@ -192,10 +194,10 @@ __global__ __launch_bounds__(1024) void llama_argmax_embed_kernel(const float* _
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const float v = __uint_as_float((uint32_t)src[c * 16 + i] << 16);
-            x[c * 16 + i] = v;
+            st_coherent(&x[c * 16 + i], v);
             sq += v * v;
         }
-        ssq[c] = sq;
+        st_coherent(&ssq[c], sq);
     }
 }
 
@@ -398,13 +400,13 @@ static void gemv_engine(const th_qweight* w, const void* x, NormArgs norm, Epi e
     if (small && w->Kp / 128 >= 64) {  // few tiles, long K (down projection): sixteen waves per tile
         const size_t smem = Q4GemvSmem<1, 16>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
-        hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 16, NORM>), dim3((unsigned)(w->Np / 16)),
+        TH_LAUNCH((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 16, NORM>), dim3((unsigned)(w->Np / 16)),
                            dim3(1024), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
                            (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm, SingleMatrix{});
     } else if (small) {
         const size_t smem = Q4GemvSmem<1, 8>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
-        hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 8, NORM>), dim3((unsigned)(w->Np / 16)),
+        TH_LAUNCH((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 8, NORM>), dim3((unsigned)(w->Np / 16)),
                            dim3(512), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
                            (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm, SingleMatrix{});
     } else if (NORM && w->Np / 16 >= 1376) {  // many tiles (gate/up, LM head): two per workgroup, one staging
@@ -414,14 +416,14 @@ static void gemv_engine(const th_qweight* w, const void* x, NormArgs norm, Epi e
         SingleMatrixTiles<2> src;
         src.tiles = (int)(w->Np / 16);
         // the two tiles streamed side by side, one reduction (+1% decode)
-        hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 4, NORM, SingleMatrixTiles<2>, 2>),
+        TH_LAUNCH((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 4, NORM, SingleMatrixTiles<2>, 2>),
                            dim3((unsigned)ceil_div(w->Np / 16, (size_t)2)), dim3(256), smem, s, (const uint4*)w->data,
                            (const _Float16*)w->scales, x, (int)w->cols, (int)w->Kp, (int)w->rows, (int)w->cols, epi,
                            norm, src);
     } else {
         const size_t smem = Q4GemvSmem<1, 4>::bytes((int)(w->Kp / 128));
         TH_REQUIRE(smem <= 64 * 1024, "engine GEMV LDS above 64 KiB");
-        hipLaunchKernelGGL((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 4, NORM>), dim3((unsigned)(w->Np / 16)),
+        TH_LAUNCH((q4_gemv_kernel<1, false, true, _Float16, Epi, 2, 4, 4, NORM>), dim3((unsigned)(w->Np / 16)),
                            dim3(256), smem, s, (const uint4*)w->data, (const _Float16*)w->scales, x, (int)w->cols,
                            (int)w->Kp, (int)w->rows, (int)w->cols, epi, norm, SingleMatrix{});
     }
@@ -449,6 +451,7 @@ struct th_llama {
     LlamaState* st = nullptr;
     int32_t* history = nullptr;
     hipGraphExec_t graph = nullptr;
+    AqlSeq* aql_step = nullptr;  // the step as a write-through AQL sequence
     bool weights_ready = false;
     // prefill workspace (rows = prompt chunk), grown on demand
     size_t pf_rows = 0;
@@ -470,6 +473,7 @@ static void llama_free(th_llama* m) {
                     m->rope_sin, m->x, m->q, m->logits, m->part, m->ssq, m->amax_v, m->att, m->sg, m->counters,
                     m->amax_i, m->st, m->history, m->pf_x, m->pf_qkv, m->pf_q, m->pf_y, m->pf_gu, m->pf_xb,
                     m->pf_att, m->pf_sg, m->pf_tok, m->pf_xe};
+    aql_free(m->aql_step);
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
@@ -495,7 +499,7 @@ static void llama_lm_head_argmax(th_llama* m, hipStream_t s) {
     NormArgs fin;
     fin.ssq = m->ssq; fin.nssq = d / 16; fin.w = m->final_norm; fin.eps = c.eps;
     gemv_engine<true>(m->lm, m->x, fin, EpiTileMax{m->logits, m->amax_v, m->amax_i, c.vocab}, s);
-    hipLaunchKernelGGL(llama_argmax_embed_kernel, dim3(1), dim3(1024), 0, s, m->amax_v, m->amax_i,
+    TH_LAUNCH(llama_argmax_embed_kernel, dim3(1), dim3(1024), 0, s, m->amax_v, m->amax_i,
                        (int)ceil_div((size_t)c.vocab, 16), m->st, m->history, m->embed, d, m->x, m->ssq);
     TH_LAUNCH_CHECK();
 }
@@ -504,7 +508,7 @@ static void llama_lm_head_argmax(th_llama* m, hipStream_t s) {
 // sets the token; decode steps chain it themselves).
 static void llama_embed_current(th_llama* m, hipStream_t s) {
     const int d = m->cfg.d_model;
-    hipLaunchKernelGGL(llama_embed_kernel, dim3((unsigned)ceil_div((size_t)d / 16, (size_t)256)), dim3(256), 0, s,
+    TH_LAUNCH(llama_embed_kernel, dim3((unsigned)ceil_div((size_t)d / 16, (size_t)256)), dim3(256), 0, s,
                        m->embed, m->st, d, m->x, m->ssq);
     TH_LAUNCH_CHECK();
 }
@@ -584,12 +588,39 @@ static bool llama_eager() {
     return eager;
 }
 
+static bool stream_capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// Every kernel of the step stores what later kernels read with write-through
+// stores (the epilogues, the attention merge, the argmax), so its AQL
+// sequence needs no release fences between kernels.
+static bool llama_use_aql(th_llama* m) {
+    return !llama_eager() && aql_enabled() && !stream_capturing(m->dev->stream);
+}
+
+static void llama_prepare_step(th_llama* m) {
+    if (llama_use_aql(m)) {
+        if (!m->aql_step) m->aql_step = aql_record(m->dev, true, [&] { llama_enqueue_step(m); });
+    } else if (!llama_eager()) {
+        llama_build_graph(m);
+    }
+}
+
+// Enqueue one step: a replay on the device's AQL queue (the caller waits
+// with aql_wait / device_sync before further stream work), or a HIP graph
+// launch when TANG_HIP_DISPATCH=graph or inside a caller's stream capture.
 static void llama_launch_step(th_llama* m) {
     if (llama_eager()) {
         llama_enqueue_step(m);
         return;
     }
-    llama_build_graph(m);
+    llama_prepare_step(m);
+    if (llama_use_aql(m)) {
+        aql_submit(*m->aql_step);
+        return;
+    }
     TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
 }
 
@@ -597,7 +628,7 @@ constexpr size_t PREFILL_CHUNK = 512;  // prompt rows per pass (workspace ~100 M
 
 static void prefill_reserve(th_llama* m, size_t rows) {
     if (rows <= m->pf_rows) return;
-    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    device_sync(m->dev);
     void* old[] = {m->pf_x, m->pf_qkv, m->pf_q, m->pf_y, m->pf_gu, m->pf_xb, m->pf_att, m->pf_sg, m->pf_tok, m->pf_xe};
     for (void* p : old)
         if (p) (void)hipFree(p);
@@ -624,7 +655,7 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
     hipStream_t s = dev->stream;
     const int d = c.d_model, ff = c.d_ff, hd = c.head_dim, W = m->qd + 2 * m->kvd;
     TH_HIP(hipMemcpyAsync(m->pf_tok, tok_host, n * 4, hipMemcpyHostToDevice, s));
-    hipLaunchKernelGGL(prefill_embed_kernel, dim3(4, (unsigned)n), dim3(256), 0, s, m->embed, m->pf_tok, d, m->pf_x);
+    TH_LAUNCH(prefill_embed_kernel, dim3(4, (unsigned)n), dim3(256), 0, s, m->embed, m->pf_tok, d, m->pf_x);
     TH_LAUNCH_CHECK();
     const size_t cache_layer = (size_t)c.max_seq * m->kvd;
     // Above 16 rows the linears run on the MFMA GEMM, whose activation layout
@@ -635,10 +666,10 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
     int* xe_sg = m->pf_xe + 2 * m->pf_rows;
     auto prefill_norm = [&](const uint16_t* w, const th_qweight* consumer) {
         if (xp)
-            hipLaunchKernelGGL(prefill_rmsnorm_kernel<true>, dim3((unsigned)n), dim3(64), 0, s, m->pf_x, w, d, c.eps,
+            TH_LAUNCH(prefill_rmsnorm_kernel<true>, dim3((unsigned)n), dim3(64), 0, s, m->pf_x, w, d, c.eps,
                                m->pf_xb, (int)consumer->Kp, xe_xb);
         else
-            hipLaunchKernelGGL(prefill_rmsnorm_kernel<false>, dim3((unsigned)n), dim3(64), 0, s, m->pf_x, w, d,
+            TH_LAUNCH(prefill_rmsnorm_kernel<false>, dim3((unsigned)n), dim3(64), 0, s, m->pf_x, w, d,
                                c.eps, m->pf_xb, d, (int*)nullptr);
         TH_LAUNCH_CHECK();
     };
@@ -655,7 +686,7 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
         _Float16* vc = m->vcache + l * cache_layer;
         prefill_norm(m->attn_norm + (size_t)l * d, m->wqkv[l]);
         linear(m->wqkv[l], m->pf_xb, xe_xb, d, m->pf_qkv, W);
-        hipLaunchKernelGGL(prefill_rope_kv_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_qkv, (int)pos0,
+        TH_LAUNCH(prefill_rope_kv_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_qkv, (int)pos0,
                            m->rope_cos, m->rope_sin, m->qd, m->kvd, hd, m->pf_q, kc, vc);
         TH_LAUNCH_CHECK();
         const bool xp_att = xp && (hd == 64 || hd == 128);
@@ -672,7 +703,7 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
             launch_q4_linear_prepared(m->wo[l], PreparedX{m->pf_att, xe_att}, n, m->pf_x, d, s, dev, true);
         } else {
             launch_q4_linear(m->wo[l], m->pf_att, TH_BF16, n, m->qd, m->pf_y, d, s, dev);
-            hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
+            TH_LAUNCH(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
             TH_LAUNCH_CHECK();
         }
         prefill_norm(m->ffn_norm + (size_t)l * d, m->wgu[l]);
@@ -680,10 +711,10 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
         if (xp) {
             const int ldo = (int)m->wd[l]->Kp;
             TH_REQUIRE(ldo * 2 <= 64 * 1024, "prefill: d_ff above 32768");
-            hipLaunchKernelGGL(prefill_swiglu_xp_kernel, dim3((unsigned)n), dim3(256), (size_t)ldo * 2, s, m->pf_gu,
+            TH_LAUNCH(prefill_swiglu_xp_kernel, dim3((unsigned)n), dim3(256), (size_t)ldo * 2, s, m->pf_gu,
                                ff, m->pf_sg, ldo, xe_sg);
         } else {
-            hipLaunchKernelGGL(prefill_swiglu_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_gu, ff, m->pf_sg,
+            TH_LAUNCH(prefill_swiglu_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_gu, ff, m->pf_sg,
                                ff);
         }
         TH_LAUNCH_CHECK();
@@ -691,7 +722,7 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
             launch_q4_linear_prepared(m->wd[l], PreparedX{m->pf_sg, xe_sg}, n, m->pf_x, d, s, dev, true);
         } else {
             linear(m->wd[l], m->pf_sg, nullptr, ff, m->pf_y, d);
-            hipLaunchKernelGGL(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
+            TH_LAUNCH(prefill_add_kernel, dim3(1024), dim3(256), 0, s, m->pf_x, m->pf_y, n * d);
             TH_LAUNCH_CHECK();
         }
     }
@@ -987,7 +1018,7 @@ int th_llama_fill_kv_synthetic(th_llama* m, size_t len, uint64_t seed) {
         th_synth_normal(th_synth_seed(seed, l, T_KCACHE), n, 1.0f, TH_F16, k[l].data());
         th_synth_normal(th_synth_seed(seed, l, T_VCACHE), n, 1.0f, TH_F16, v[l].data());
     }
-    TH_HIP(hipStreamSynchronize(m->dev->stream));  // the engine stream is non-blocking: drain it first
+    device_sync(m->dev);  // the engine stream is non-blocking: drain it first
     for (size_t l = 0; l < L; l++) {
         TH_HIP(hipMemcpy(m->kcache + l * layer, k[l].data(), n * 2, hipMemcpyHostToDevice));
         TH_HIP(hipMemcpy(m->vcache + l * layer, v[l].data(), n * 2, hipMemcpyHostToDevice));
@@ -999,7 +1030,7 @@ int th_llama_set_token(th_llama* m, int32_t token) {
     TH_API_BEGIN
     TH_REQUIRE(m, "null model");
     TH_REQUIRE(token >= 0 && token < m->cfg.vocab, "token out of range");
-    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    device_sync(m->dev);
     LlamaState s{};
     TH_HIP(hipMemcpy(&s, m->st, sizeof s, hipMemcpyDeviceToHost));
     s.token = token;
@@ -1013,13 +1044,14 @@ int th_llama_step_device(th_llama* m, size_t pos) {
     TH_REQUIRE(m && m->weights_ready, "model not initialised");
     TH_REQUIRE(pos < (size_t)m->cfg.max_seq, "position beyond max_seq");
     LlamaState s{};
-    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    device_sync(m->dev);
     TH_HIP(hipMemcpy(&s, m->st, sizeof s, hipMemcpyDeviceToHost));
     s.pos = (int)pos;
     s.step = 0;
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
     llama_embed_current(m, m->dev->stream);
     llama_launch_step(m);
+    aql_wait(m->dev);
     TH_API_END
 }
 
@@ -1031,11 +1063,11 @@ int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, in
     TH_REQUIRE(n_steps <= (size_t)m->max_steps, "too many steps");
     if (n_steps == 0) return TH_OK;
     LlamaState s{(int)pos, token, 0, 0};
-    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    device_sync(m->dev);
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
     llama_embed_current(m, m->dev->stream);
     for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
-    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    device_sync(m->dev);
     if (tokens_out) TH_HIP(hipMemcpy(tokens_out, m->history, n_steps * 4, hipMemcpyDeviceToHost));
     if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
     TH_API_END
@@ -1054,14 +1086,15 @@ int th_llama_generate_sampled(th_llama* m, th_sampler* smp, const int32_t* promp
     std::vector<int32_t> past(prompt, prompt + n_prompt);  // generate() passes every token so far
     std::vector<float> logits((size_t)m->cfg.vocab);
     LlamaState st{(int)pos, prompt[n_prompt - 1], 0, 0};
-    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    device_sync(m->dev);
     TH_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
     hipStream_t s = m->dev->stream;  // non-blocking: every copy goes on it and is waited for
     llama_embed_current(m, s);
     for (size_t i = 0; i < c.max_tokens; i++) {
         llama_launch_step(m);  // advances the device position; its greedy token is replaced below
+        aql_wait(m->dev);
         TH_HIP(hipMemcpyAsync(logits.data(), m->logits, logits.size() * 4, hipMemcpyDeviceToHost, s));
-        TH_HIP(hipStreamSynchronize(s));
+        device_sync(m->dev);
         int32_t next = 0;
         check_status(th_sampler_sample(smp, logits.data(), logits.size(), past.data(), past.size(), &next));
         if (c.stop_token >= 0 && next == c.stop_token) break;  // sampling.rs:246-250
@@ -1069,7 +1102,7 @@ int th_llama_generate_sampled(th_llama* m, th_sampler* smp, const int32_t* promp
         tokens_out[(*n_out)++] = next;
         TH_HIP(hipMemcpyAsync(&m->st->token, &next, sizeof next, hipMemcpyHostToDevice, s));
         llama_embed_current(m, s);  // the sampled token replaces the greedy one the step embedded
-        TH_HIP(hipStreamSynchronize(s));
+        device_sync(m->dev);
     }
     TH_API_END
 }
@@ -1086,18 +1119,18 @@ int th_llama_prefill(th_llama* m, const int32_t* tokens, size_t n, size_t pos, i
     for (size_t c0 = 0; c0 < n; c0 += PREFILL_CHUNK) {
         rows = std::min(PREFILL_CHUNK, n - c0);
         prefill_chunk(m, tokens + c0, rows, pos + c0);
-        TH_HIP(hipStreamSynchronize(s));  // the token chunk is copied from the caller's memory
+        device_sync(m->dev);  // the token chunk is copied from the caller's memory
     }
     // the last row: final norm, LM head and argmax as a decode step would
     const th_llama_config& c = m->cfg;
     const int d = c.d_model;
     LlamaState st{(int)(pos + n - 1), tokens[n - 1], 0, 0};
     TH_HIP(hipMemcpyAsync(m->st, &st, sizeof st, hipMemcpyHostToDevice, s));
-    hipLaunchKernelGGL(prefill_last_row_kernel, dim3((unsigned)ceil_div((size_t)d / 16, (size_t)256)), dim3(256), 0, s,
+    TH_LAUNCH(prefill_last_row_kernel, dim3((unsigned)ceil_div((size_t)d / 16, (size_t)256)), dim3(256), 0, s,
                        m->pf_x + (rows - 1) * (size_t)d, d, m->x, m->ssq);
     TH_LAUNCH_CHECK();
     llama_lm_head_argmax(m, s);
-    TH_HIP(hipStreamSynchronize(s));
+    device_sync(m->dev);
     if (next_token) TH_HIP(hipMemcpy(next_token, m->history, 4, hipMemcpyDeviceToHost));
     if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost));
     TH_API_END
@@ -1121,15 +1154,22 @@ int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, 
     TH_REQUIRE(token >= 0 && token < m->cfg.vocab, "token out of range");
     TH_REQUIRE(pos + n_steps <= (size_t)m->cfg.max_seq, "generation runs past max_seq");
     LlamaState s{(int)pos, token, 0, 0};
-    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    device_sync(m->dev);
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
     llama_embed_current(m, m->dev->stream);
-    if (!llama_eager()) llama_build_graph(m);
-    TH_HIP(hipEventRecord(m->dev->ev_start, m->dev->stream));
-    for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
-    TH_HIP(hipEventRecord(m->dev->ev_stop, m->dev->stream));
-    TH_HIP(hipEventSynchronize(m->dev->ev_stop));
-    TH_HIP(hipEventElapsedTime(ms, m->dev->ev_start, m->dev->ev_stop));
+    llama_prepare_step(m);
+    if (llama_use_aql(m)) {  // device clock stamps around the replays
+        aql_stamp(m->dev, 0);
+        for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
+        aql_stamp(m->dev, 1);
+        *ms = aql_stamped_ms(m->dev);
+    } else {
+        TH_HIP(hipEventRecord(m->dev->ev_start, m->dev->stream));
+        for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
+        TH_HIP(hipEventRecord(m->dev->ev_stop, m->dev->stream));
+        TH_HIP(hipEventSynchronize(m->dev->ev_stop));
+        TH_HIP(hipEventElapsedTime(ms, m->dev->ev_start, m->dev->ev_stop));
+    }
     TH_API_END
 }
 

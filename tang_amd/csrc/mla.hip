@@ -466,7 +466,7 @@ static void launch_mla_attn_w(dim3 grid, size_t lds, hipStream_t s, const uint16
             granted = lds;
         }
     }
-    hipLaunchKernelGGL(mla_attn_kernel<W>, grid, dim3(MLA_THREADS), lds, s, qa, cache, L, R, sm_scale, n_splits, part);
+    TH_LAUNCH(mla_attn_kernel<W>, grid, dim3(MLA_THREADS), lds, s, qa, cache, L, R, sm_scale, n_splits, part);
 }
 
 template <int... Ks>
@@ -519,7 +519,7 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     uint16_t* qa = (uint16_t*)ws;
     float* part = (float*)(ws + round_up(qa_bytes, 256));
     // 1. absorb
-    hipLaunchKernelGGL(mla_absorb_kernel, dim3((unsigned)ceil_div(H * r / 16, (size_t)4)), dim3(256), 0, s,
+    TH_LAUNCH(mla_absorb_kernel, dim3((unsigned)ceil_div(H * r / 16, (size_t)4)), dim3(256), 0, s,
                        (const uint8_t*)w_uk->data, (const float*)w_uk->scales, (int)r, (int)dn, (int)(w_uk->Kp / 64),
                        (int)B, (const float*)q_nope->ptr, (const float*)q_rope->ptr, (int)dr, qa);
     TH_LAUNCH_CHECK();
@@ -532,7 +532,7 @@ extern "C" int th_mla_decode(th_device* dev, const th_buffer* q_nope, const th_b
     TH_LAUNCH_CHECK();
     // 3. merge + up-projection
     const unsigned groups = (unsigned)ceil_div(dv / 16, (size_t)4);  // four 16-row tiles per workgroup
-    hipLaunchKernelGGL(mla_merge_up_kernel, dim3((unsigned)H, (unsigned)B, groups), dim3(MLA_UP_THREADS), 0, s, part,
+    TH_LAUNCH(mla_merge_up_kernel, dim3((unsigned)H, (unsigned)B, groups), dim3(MLA_UP_THREADS), 0, s, part,
                        n_splits, (int)r, (const uint8_t*)w_uv->data, (const float*)w_uv->scales, (int)dv,
                        (int)(w_uv->Kp / 64), (float*)out->ptr);
     TH_LAUNCH_CHECK();

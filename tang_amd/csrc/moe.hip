@@ -577,7 +577,7 @@ static void moe_grouped_gemv(const th_moe* m, const th_qweight* w0, const uint4*
             done = smem;
         }
     }
-    hipLaunchKernelGGL(k, dim3((unsigned)(max_work * wg_per_item)), dim3(64 * NW), smem, m->dev->stream, (const uint4*)nullptr,
+    TH_LAUNCH(k, dim3((unsigned)(max_work * wg_per_item)), dim3(64 * NW), smem, m->dev->stream, (const uint4*)nullptr,
                        (const _Float16*)nullptr, (const void*)x, (int)w0->cols, (int)w0->Kp, (int)w0->rows,
                        (int)w0->cols, epi, NormArgs{}, src);
     TH_LAUNCH_CHECK();
@@ -594,7 +594,7 @@ static void moe_grouped_gemm(const th_moe* m, const th_qweight* w0, const uint4*
     const PreparedX xp = prepare_x(m->dev, x, false, x_rows, w0->cols, w0->cols, w0->Kp, m->dev->stream);
     MoeGemmSrc src{m->work, data, scales, wexps, slot_token};
     const unsigned gx = (unsigned)ceil_div(w0->Np / 16, (size_t)(4 * MOE_GEMM_RT));
-    hipLaunchKernelGGL((q4_gemm_mfma_kernel<MOE_GEMM_RT, MOE_GEMM_CB, _Float16, MoeGemmSrc, Epi>),
+    TH_LAUNCH((q4_gemm_mfma_kernel<MOE_GEMM_RT, MOE_GEMM_CB, _Float16, MoeGemmSrc, Epi>),
                        dim3(gx, (unsigned)max_work, 1), dim3(256), 0, m->dev->stream, (const uint4*)nullptr,
                        (const _Float16*)nullptr, (const int*)nullptr, xp.x, xp.xexp, epi, src, (int)w0->rows,
                        (int)w0->cols, (int)w0->Kp, (int)w0->Kp, (int)(w0->Kp / 128));
@@ -685,18 +685,18 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
     const bool gemm = T > (size_t)MOE_SMALL_T;  // prefill-sized: grouped MFMA GEMM, 64-slot work items
     const int rows = gemm ? MOE_GEMM_CB * 16 : MOE_MIN_ROWS;
     const size_t max_work = moe_max_work(m, T, rows);
-    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)ceil_div(T, ROUTER_TOK), (unsigned)ceil_div(m->E, ROUTER_EXP)),
+    TH_LAUNCH(moe_router_kernel, dim3((unsigned)ceil_div(T, ROUTER_TOK), (unsigned)ceil_div(m->E, ROUTER_EXP)),
                        dim3(256), 0, s, (const uint16_t*)h->ptr, m->router, (int)T, (int)m->E, (int)m->d, m->logits);
     TH_LAUNCH_CHECK();
     const bool fused = T * m->k <= (size_t)MOE_FUSED_ENTRIES && T <= (size_t)MOE_SMALL_T;  // top-k inside dispatch
     auto route = [&](auto pl_tag) {  // top-k and dispatch with ceil(E / 64) expert slots per lane
         constexpr int PL = decltype(pl_tag)::value;
         if (!fused) {
-            hipLaunchKernelGGL(moe_topk_kernel<PL>, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, s, m->logits, (int)T,
+            TH_LAUNCH(moe_topk_kernel<PL>, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, s, m->logits, (int)T,
                                (int)m->E, (int)m->k, (int32_t*)topk_idx->ptr, (float*)topk_w->ptr);
             TH_LAUNCH_CHECK();
         }
-        hipLaunchKernelGGL(moe_dispatch_kernel<PL>, dim3(1), dim3(1024), 0, s, fused ? (const float*)m->logits : nullptr,
+        TH_LAUNCH(moe_dispatch_kernel<PL>, dim3(1), dim3(1024), 0, s, fused ? (const float*)m->logits : nullptr,
                            (int32_t*)topk_idx->ptr, (float*)topk_w->ptr, (const int32_t*)topk_idx->ptr, (int)T, (int)m->k,
                            (int)m->E, (int)m->S, rows, m->offsets, m->slot_token, m->token_slot, m->work, (int)max_work);
         TH_LAUNCH_CHECK();
@@ -720,7 +720,7 @@ int th_moe_forward(th_moe* m, const th_buffer* h, size_t T, th_buffer* out, th_b
                          max_work,
                          EpiGemmMoeStore{m->ybuf, (int)m->d});
     }
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)ceil_div(m->d, (size_t)1024)), dim3(256), 0, s, m->ybuf, m->token_slot,
+    TH_LAUNCH(moe_combine_kernel, dim3((unsigned)T, (unsigned)ceil_div(m->d, (size_t)1024)), dim3(256), 0, s, m->ybuf, m->token_slot,
                        (const float*)topk_w->ptr, m->offsets, (int)m->k, (int)m->E, (int)m->S, (int)m->d,
                        (float*)out->ptr);
     TH_LAUNCH_CHECK();

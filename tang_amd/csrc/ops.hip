@@ -140,7 +140,7 @@ int th_buffer_zero(th_buffer* b) {
     if (bytes == 0) return TH_OK;
     // A fill kernel, not hipMemsetAsync, so the call is safe inside graph capture.
     if (bytes % 4 == 0) {
-        hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(bytes / 4)), dim3(256), 0, b->dev->stream,
+        TH_LAUNCH(fill_zero_kernel, dim3(grid_for(bytes / 4)), dim3(256), 0, b->dev->stream,
                            (uint32_t*)b->ptr, bytes / 4);
         TH_LAUNCH_CHECK();
     } else {
@@ -156,7 +156,7 @@ int th_convert(th_device* dev, const th_buffer* src, th_buffer* dst) {
     TH_REQUIRE(ok(src->dtype) && ok(dst->dtype), "convert supports f32, bf16 and f16");
     TH_REQUIRE(dst->n >= src->n, "destination too small");
     if (src->n == 0) return TH_OK;
-    hipLaunchKernelGGL(convert_kernel, dim3(grid_for(src->n)), dim3(256), 0, dev->stream, src->ptr, src->dtype,
+    TH_LAUNCH(convert_kernel, dim3(grid_for(src->n)), dim3(256), 0, dev->stream, src->ptr, src->dtype,
                        dst->ptr, dst->dtype, src->n);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -170,7 +170,7 @@ int th_rms_norm(th_device* dev, const th_buffer* x, const th_buffer* w, size_t g
     require_len_any(w, dim, "weight");
     require_len(out, TH_F32, groups * dim, "out");
     if (groups * dim == 0) return TH_OK;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)groups), dim3(256), 0, dev->stream, (const float*)x->ptr,
+    TH_LAUNCH(rms_norm_kernel, dim3((unsigned)groups), dim3(256), 0, dev->stream, (const float*)x->ptr,
                        w->ptr, weight_flag(w), (int)dim, eps, (float*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -186,7 +186,7 @@ int th_rms_norm_residual(th_device* dev, const th_buffer* in, const th_buffer* r
     require_len(out, TH_F32, groups * dim, "out");
     require_len(sum_out, TH_F32, groups * dim, "sum_out");
     if (groups * dim == 0) return TH_OK;
-    hipLaunchKernelGGL(rms_norm_residual_kernel, dim3((unsigned)groups), dim3(256), 0, dev->stream,
+    TH_LAUNCH(rms_norm_residual_kernel, dim3((unsigned)groups), dim3(256), 0, dev->stream,
                        (const float*)in->ptr, (const float*)res->ptr, w->ptr, weight_flag(w), (int)dim, eps,
                        (float*)out->ptr, (float*)sum_out->ptr);
     TH_LAUNCH_CHECK();
@@ -212,7 +212,7 @@ int th_rope_forward(th_device* dev, const th_buffer* in, const th_buffer* cs, co
     require_len(cs, TH_F32, (start_pos + seq_len) * (head_dim / 2), "cos table");
     require_len(sn, TH_F32, (start_pos + seq_len) * (head_dim / 2), "sin table");
     if (n == 0) return TH_OK;
-    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(n / 2)), dim3(256), 0, dev->stream, (const float*)in->ptr,
+    TH_LAUNCH(rope_kernel, dim3(grid_for(n / 2)), dim3(256), 0, dev->stream, (const float*)in->ptr,
                        (const float*)cs->ptr, (const float*)sn->ptr, (int)seq_len, (int)n_heads, (int)head_dim,
                        (int)start_pos, (float*)out->ptr);
     TH_LAUNCH_CHECK();
@@ -226,7 +226,7 @@ int th_swiglu(th_device* dev, const th_buffer* g, const th_buffer* u, size_t n, 
     require_len(u, TH_F32, n, "up");
     require_len(out, TH_F32, n, "out");
     if (n == 0) return TH_OK;
-    hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(n)), dim3(256), 0, dev->stream, (const float*)g->ptr,
+    TH_LAUNCH(swiglu_kernel, dim3(grid_for(n)), dim3(256), 0, dev->stream, (const float*)g->ptr,
                        (const float*)u->ptr, n, (float*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -239,7 +239,7 @@ int th_add(th_device* dev, const th_buffer* a, const th_buffer* b, size_t n, th_
     require_len(b, TH_F32, n, "b");
     require_len(out, TH_F32, n, "out");
     if (n == 0) return TH_OK;
-    hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, dev->stream, (const float*)a->ptr,
+    TH_LAUNCH(add_kernel, dim3(grid_for(n)), dim3(256), 0, dev->stream, (const float*)a->ptr,
                        (const float*)b->ptr, n, (float*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -263,7 +263,7 @@ int th_embedding(th_device* dev, const th_buffer* w, const th_buffer* ids, size_
     const size_t vocab = w->n / dim;
     for (size_t i = 0; i < seq_len; i++) TH_REQUIRE(h[i] < vocab, "token id out of range");
     if (seq_len * dim == 0) return TH_OK;
-    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(seq_len * dim)), dim3(256), 0, dev->stream, w->ptr,
+    TH_LAUNCH(embedding_kernel, dim3(grid_for(seq_len * dim)), dim3(256), 0, dev->stream, w->ptr,
                        weight_flag(w), (const uint32_t*)ids->ptr, (int)seq_len, (int)dim, (float*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -275,7 +275,7 @@ int th_softmax(th_device* dev, const th_buffer* x, size_t rows, size_t len, th_b
     require_len(x, TH_F32, rows * len, "x");
     require_len(out, TH_F32, rows * len, "out");
     if (rows * len == 0) return TH_OK;
-    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)rows), dim3(256), 0, dev->stream, (const float*)x->ptr, (int)len,
+    TH_LAUNCH(softmax_kernel, dim3((unsigned)rows), dim3(256), 0, dev->stream, (const float*)x->ptr, (int)len,
                        (float*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
@@ -289,7 +289,7 @@ int th_argmax(th_device* dev, const th_buffer* x, size_t rows, size_t n, th_buff
     TH_REQUIRE(out->dtype == TH_U32 || out->dtype == TH_I32, "out must be u32");
     require_len_any(out, rows, "out");
     if (rows == 0) return TH_OK;
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, dev->stream, (const float*)x->ptr, (int)n,
+    TH_LAUNCH(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, dev->stream, (const float*)x->ptr, (int)n,
                        (uint32_t*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END

@@ -111,7 +111,7 @@ struct EpiStore {
     static constexpr bool HAS_FINISH = false;
     float* y; int ldy;
     __device__ __forceinline__ void operator()(int m, int n, float v, const float* tile, float*) const {
-        y[(size_t)m * ldy + n] = v;
+        st_coherent(&y[(size_t)m * ldy + n], v);
     }
     __device__ __forceinline__ void finish(int, int, const float*, int) const {}
 };

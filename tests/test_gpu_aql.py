@@ -1,0 +1,107 @@
+"""Replay on the library's own AQL queue (tang_amd/csrc/aql.cpp) against HIP
+launches of the same kernels: identical outputs, bit for bit.
+
+The decode step and the benchmarked GEMV chain replay as AQL sequences with
+no release fences between kernels (their kernels store what later kernels
+read write-through); TANG_HIP_DISPATCH=graph switches the engine back to a
+HIP graph, which a child process runs here for the comparison.
+"""
+import ctypes
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from llama_ref import CONFIG_SMALL, device_generate, device_llama
+from tang_amd import capi
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_q4_gemv_aql_chain_matches_stream(dev, m):
+    """A 30-launch chain over three weight matrices (different values) on the
+    AQL queue leaves the output of the last launch, as launches on the
+    stream do."""
+    print(f"aql gemv m={m}", flush=True)
+    N, K = 1000, 2048
+    ws = []
+    for s in (5, 6, 7):
+        nib, sc = capi.synth_q4(s, N, K)
+        ws.append(dev.q4_upload_packed(nib, sc, N, K, capi.F16))
+    x = dev.upload(capi.synth_normal(9, m * K, 1.0, capi.BF16), capi.BF16)
+    y = dev.alloc(m * N)
+    try:
+        dev.bench_linear(x, m, ws, y, 30)
+        ref = y.to_numpy().copy()
+        for rep in range(2):
+            y.upload(np.zeros(m * N, np.float32))
+            ms = dev.bench_linear(x, m, ws, y, 30, use_graph="aql")
+            assert ms > 0
+            assert np.array_equal(y.to_numpy(), ref), rep
+        # launch 29 reads ws[2]: a one-launch stream call on ws[2] agrees
+        y2 = dev.alloc(m * N)
+        dev.bench_linear(x, m, [ws[2]], y2, 1)
+        assert np.array_equal(y2.to_numpy(), ref)
+    finally:
+        for w in ws:
+            w.free()
+
+
+def test_q8_gemv_aql_chain_matches_stream(dev):
+    """q8 kernels are recorded with agent-scope fences kept (their epilogue
+    is not write-through): same outputs."""
+    q, rs = capi.synth_q8_rowwise(1, 512, 1024)
+    ws = [dev.q8_upload_rowwise(q, rs, 512, 1024) for _ in range(2)]
+    x = dev.upload(capi.synth_normal(11, 1024, 1.0, capi.F32))
+    y = dev.alloc(512)
+    try:
+        dev.bench_linear(x, 1, ws, y, 8)
+        ref = y.to_numpy().copy()
+        y.upload(np.zeros(512, np.float32))
+        dev.bench_linear(x, 1, ws, y, 8, use_graph="aql")
+        assert np.array_equal(y.to_numpy(), ref)
+    finally:
+        for w in ws:
+            w.free()
+
+
+_CHILD = r"""
+import sys, numpy as np
+sys.path.insert(0, {here!r}); sys.path.insert(0, {root!r})
+from llama_ref import CONFIG_SMALL, device_generate, device_llama
+from tang_amd import capi
+dev = capi.HipComputeDevice(0)
+m = device_llama(dev, CONFIG_SMALL, 7, 8, 100)
+toks, logits = device_generate(m, CONFIG_SMALL, 1, 100, 48)
+capi.lib().th_llama_destroy(m)
+dev.close()
+np.savez({out!r}, toks=toks, logits=logits)
+"""
+
+
+def test_decode_aql_matches_hip_graph(dev, tmp_path):
+    """48 greedy steps of the small model: tokens and final logits from the
+    AQL replay (this process) equal the HIP graph replay's (a child process
+    with TANG_HIP_DISPATCH=graph) bit for bit."""
+    cfg = CONFIG_SMALL
+    m = device_llama(dev, cfg, 7, 8, 100)
+    try:
+        toks, logits = device_generate(m, cfg, 1, 100, 48)
+        ms = ctypes.c_float()
+        capi.check(capi.lib().th_llama_time_steps(m, 1, 100, 4, ctypes.byref(ms)))
+        assert 0 < ms.value < 1e4
+    finally:
+        capi.lib().th_llama_destroy(m)
+    out = str(tmp_path / "graph.npz")
+    env = dict(os.environ, TANG_HIP_DISPATCH="graph")
+    code = _CHILD.format(here=HERE, root=os.path.dirname(HERE), out=out)
+    print("child: graph dispatch", flush=True)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0, r.stderr[-2000:]
+    g = np.load(out)
+    assert np.array_equal(g["toks"], toks)
+    assert np.array_equal(g["logits"], logits)
