@@ -72,6 +72,10 @@ struct KernelInfo {
 // Per-process: the code objects of this library, loaded once per agent.
 struct Program {
     hsa_agent_t agent{};
+    // the code object images stay alive with the executables: the loader
+    // reports their memory as the loaded code objects' storage
+    // (hsa_ven_amd_loader), so it must stay valid
+    std::vector<std::string> images;
     std::vector<hsa_executable_t> exes;
     std::unordered_map<std::string, KernelInfo> by_name;
     std::unordered_map<const void*, KernelInfo> by_handle;
@@ -190,7 +194,8 @@ Program* program_for(hsa_agent_t agent) {
         if (p->agent.handle == agent.handle) return p;
     Program* p = new Program;
     p->agent = agent;
-    for (const std::string& co : own_code_objects()) {
+    p->images = own_code_objects();
+    for (const std::string& co : p->images) {
         hsa_code_object_reader_t rd;
         TH_HSA(hsa_code_object_reader_create_from_memory(co.data(), co.size(), &rd));
         hsa_executable_t ex;
@@ -420,7 +425,11 @@ void aql_submit(const AqlSeq& seq) {
                                 (1 << HSA_PACKET_HEADER_BARRIER) | (acq << HSA_PACKET_HEADER_ACQUIRE_FENCE_SCOPE) |
                                 (rel << HSA_PACKET_HEADER_RELEASE_FENCE_SCOPE);
         __atomic_store_n((uint32_t*)pk, (uint32_t)header | ((uint32_t)setup << 16), __ATOMIC_RELEASE);
-        if ((i & 255) == 255) hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
+        // doorbell every 256 packets, and at the ring's last slot, so that no
+        // rung batch wraps around the end of the ring (queue interceptors,
+        // such as a profiler's, copy a rung batch as one range)
+        if ((i & 255) == 255 || ((idx + 1) & (q->size - 1)) == 0)
+            hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
     }
     hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
 }
