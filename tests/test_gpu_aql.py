@@ -51,6 +51,30 @@ def test_q4_gemv_aql_chain_matches_stream(dev, m):
             w.free()
 
 
+def test_aql_sequence_longer_than_the_queue(dev):
+    """One sequence of 5000 launches (the queue holds 4096 packets): the
+    submission waits for ring space and wraps around the ring's end, and
+    rings the doorbell at its last slot; the last launch's output equals the
+    stream's."""
+    N, K = 256, 512
+    nib, sc = capi.synth_q4(21, N, K)
+    ws = [dev.q4_upload_packed(nib, sc, N, K, capi.F16)]
+    nib2, sc2 = capi.synth_q4(22, N, K)
+    ws.append(dev.q4_upload_packed(nib2, sc2, N, K, capi.F16))
+    x = dev.upload(capi.synth_normal(23, K, 1.0, capi.BF16), capi.BF16)
+    y = dev.alloc(N)
+    try:
+        dev.bench_linear(x, 1, ws, y, 5000)
+        ref = y.to_numpy().copy()
+        for rep in range(2):
+            y.upload(np.zeros(N, np.float32))
+            dev.bench_linear(x, 1, ws, y, 5000, use_graph="aql")
+            assert np.array_equal(y.to_numpy(), ref), rep
+    finally:
+        for w in ws:
+            w.free()
+
+
 def test_q8_gemv_aql_chain_matches_stream(dev):
     """q8 kernels are recorded with agent-scope fences kept (their epilogue
     is not write-through): same outputs."""
