@@ -63,13 +63,13 @@ Q8_BYTES = 4096 * 4096 + 3 * 4096 * 4  # config 1: W, row scales, x, y
 
 def q8_bench(dev, steps, copies=18):
     """Config 1: int8 4096x4096 GEMV, per-row scales, f32 x (18 copies =
-    302 MB > MALL), graph-launched."""
+    302 MB > MALL), replayed as one sequence on the library's AQL queue."""
     q, rs = capi.synth_q8_rowwise(1, 4096, 4096)
     ws = [dev.q8_upload_rowwise(q, rs, 4096, 4096) for _ in range(copies)]
     x = dev.upload(capi.synth_normal(11, 4096, 1.0, capi.F32))
     y = dev.alloc(4096)
     dev.bench_linear(x, 1, ws, y, 48)
-    ms = dev.bench_linear(x, 1, ws, y, steps, use_graph=True)
+    ms = dev.bench_linear(x, 1, ws, y, steps, use_graph="aql")
     for w in ws:
         w.free()
     us = ms * 1e3 / steps

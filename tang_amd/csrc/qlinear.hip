@@ -377,9 +377,9 @@ int th_bench_linear(th_device* dev, const th_buffer* x, size_t m, th_qweight* co
     call(0);  // sizes the workspace before any capture
     TH_HIP(hipStreamSynchronize(dev->stream));
     if (use_graph == 2) {
-        // The q4 GEMV (m <= 16) stores its output write-through: no release
-        // fences between the launches.
-        const bool wt = w0->bits == 4 && m <= 16;
+        // The GEMVs (q8, and q4 at m <= 16) store their output write-through:
+        // no release fences between the launches.
+        const bool wt = w0->bits == 8 || m <= 16;
         AqlSeq* seq = aql_record(dev, wt, [&] {
             for (size_t i = 0; i < iters; i++) call(i);
         });

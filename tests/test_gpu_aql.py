@@ -76,8 +76,8 @@ def test_aql_sequence_longer_than_the_queue(dev):
 
 
 def test_q8_gemv_aql_chain_matches_stream(dev):
-    """q8 kernels are recorded with agent-scope fences kept (their epilogue
-    is not write-through): same outputs."""
+    """The q8 GEMV chain (write-through outputs, no release fences) on the
+    AQL queue: same outputs as on the stream."""
     q, rs = capi.synth_q8_rowwise(1, 512, 1024)
     ws = [dev.q8_upload_rowwise(q, rs, 512, 1024) for _ in range(2)]
     x = dev.upload(capi.synth_normal(11, 1024, 1.0, capi.F32))
