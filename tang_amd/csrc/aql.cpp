@@ -382,14 +382,15 @@ void aql_free(AqlSeq* seq) {
     delete seq;
 }
 
-void aql_submit(const AqlSeq& seq) {
+void aql_submit(const AqlSeq& seq, size_t repeat) {
     th_device* d = seq.dev;
     AqlDev* a = aql_dev(d);
     TH_REQUIRE(!a->error.load(), "AQL queue is in an error state");
     // earlier HIP work on the device stream comes first
     if (!a->in_flight) TH_HIP(hipStreamSynchronize(d->stream));
     hsa_queue_t* q = a->queue;
-    const size_t n = seq.packets.size();
+    const size_t np = seq.packets.size(), n = np * repeat;
+    if (n == 0) return;
     // Inside a write-through sequence: no release (the values later kernels
     // read are already at the coherence point), but the agent-scope acquire
     // stays: it invalidates the XCD L2s, which may hold lines a kernel read
@@ -403,7 +404,7 @@ void aql_submit(const AqlSeq& seq) {
     uint64_t idx = 0;
     const double t0 = now_s();
     for (size_t i = 0; i < n; i++) {
-        const AqlPacket& p = seq.packets[i];
+        const AqlPacket& p = seq.packets[i % np];
         idx = hsa_queue_add_write_index_relaxed(q, 1);
         while (idx - hsa_queue_load_read_index_scacquire(q) >= q->size) {
             if (a->error.load() || now_s() - t0 > WAIT_LIMIT_S) throw Error(TH_ERR_HIP, "AQL queue does not drain");

@@ -17,7 +17,9 @@ bool aql_enabled();
 AqlSeq* aql_record(th_device* d, bool write_through, const std::function<void()>& enqueue);
 // Enqueue a replay, after earlier submissions (and after the device stream's
 // work when nothing is in flight).  Call aql_wait before further stream work.
-void aql_submit(const AqlSeq& seq);
+// repeat: the sequence `repeat` times back to back as one submission
+// (system-scope fences only at its first and last packet).
+void aql_submit(const AqlSeq& seq, size_t repeat = 1);
 // Wait for every submitted sequence of the device.
 void aql_wait(th_device* d);
 void aql_free(AqlSeq* seq);

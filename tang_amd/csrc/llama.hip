@@ -611,18 +611,23 @@ static void llama_prepare_step(th_llama* m) {
 // Enqueue one step: a replay on the device's AQL queue (the caller waits
 // with aql_wait / device_sync before further stream work), or a HIP graph
 // launch when TANG_HIP_DISPATCH=graph or inside a caller's stream capture.
-static void llama_launch_step(th_llama* m) {
+static void llama_launch_steps(th_llama* m, size_t n) {
     if (llama_eager()) {
-        llama_enqueue_step(m);
+        for (size_t i = 0; i < n; i++) llama_enqueue_step(m);
         return;
     }
     llama_prepare_step(m);
     if (llama_use_aql(m)) {
-        aql_submit(*m->aql_step);
+        // n steps with no host work between them: one submission, so the
+        // token boundaries carry the sequence's own fences (every kernel of
+        // the step stores write-through) rather than system-scope ones
+        aql_submit(*m->aql_step, n);
         return;
     }
-    TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
+    for (size_t i = 0; i < n; i++) TH_HIP(hipGraphLaunch(m->graph, m->dev->stream));
 }
+
+static void llama_launch_step(th_llama* m) { llama_launch_steps(m, 1); }
 
 constexpr size_t PREFILL_CHUNK = 512;  // prompt rows per pass (workspace ~100 MB at the 7B shape)
 
@@ -1066,7 +1071,7 @@ int th_llama_generate(th_llama* m, int32_t token, size_t pos, size_t n_steps, in
     device_sync(m->dev);
     TH_HIP(hipMemcpy(m->st, &s, sizeof s, hipMemcpyHostToDevice));
     llama_embed_current(m, m->dev->stream);
-    for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
+    llama_launch_steps(m, n_steps);
     device_sync(m->dev);
     if (tokens_out) TH_HIP(hipMemcpy(tokens_out, m->history, n_steps * 4, hipMemcpyDeviceToHost));
     if (last_logits) TH_HIP(hipMemcpy(last_logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
@@ -1160,12 +1165,12 @@ int th_llama_time_steps(th_llama* m, int32_t token, size_t pos, size_t n_steps, 
     llama_prepare_step(m);
     if (llama_use_aql(m)) {  // device clock stamps around the replays
         aql_stamp(m->dev, 0);
-        for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
+        llama_launch_steps(m, n_steps);
         aql_stamp(m->dev, 1);
         *ms = aql_stamped_ms(m->dev);
     } else {
         TH_HIP(hipEventRecord(m->dev->ev_start, m->dev->stream));
-        for (size_t i = 0; i < n_steps; i++) llama_launch_step(m);
+        llama_launch_steps(m, n_steps);
         TH_HIP(hipEventRecord(m->dev->ev_stop, m->dev->stream));
         TH_HIP(hipEventSynchronize(m->dev->ev_stop));
         TH_HIP(hipEventElapsedTime(ms, m->dev->ev_start, m->dev->ev_stop));
