@@ -211,7 +211,9 @@ Program* program_for(hsa_agent_t agent) {
     return p;
 }
 
-const KernelInfo& kernel_info(Program* p, const void* handle) {
+// Under g_mu (recordings on several threads share the per-agent cache).
+KernelInfo kernel_info(Program* p, const void* handle) {
+    std::lock_guard<std::mutex> lock(g_mu);
     auto it = p->by_handle.find(handle);
     if (it != p->by_handle.end()) return it->second;
     Dl_info di{};
@@ -304,7 +306,7 @@ static AqlDev* aql_dev(th_device* d) {
 void aql_record_launch(AqlSeq* seq, const void* kernel, dim3 grid, dim3 block, size_t shmem, const void* args,
                        size_t bytes) {
     AqlDev* a = aql_dev(seq->dev);
-    const KernelInfo& k = kernel_info(a->prog, kernel);
+    const KernelInfo k = kernel_info(a->prog, kernel);
     const size_t explicit_end = round_up(bytes, 8);
     size_t seg = std::max<size_t>(k.kernarg_bytes, bytes);
     const bool hidden = k.kernarg_bytes > explicit_end;
@@ -405,10 +407,16 @@ void aql_submit(const AqlSeq& seq, size_t repeat) {
     const double t0 = now_s();
     for (size_t i = 0; i < n; i++) {
         const AqlPacket& p = seq.packets[i % np];
-        idx = hsa_queue_add_write_index_relaxed(q, 1);
+        // one producer (this thread): wait for a free slot, then take it, so a
+        // failed wait leaves no reserved slot unwritten
+        idx = hsa_queue_load_write_index_relaxed(q);
         while (idx - hsa_queue_load_read_index_scacquire(q) >= q->size) {
-            if (a->error.load() || now_s() - t0 > WAIT_LIMIT_S) throw Error(TH_ERR_HIP, "AQL queue does not drain");
+            if (a->error.load() || now_s() - t0 > WAIT_LIMIT_S) {
+                a->error.store(1);  // its sequence is cut short: the queue is unusable from here
+                throw Error(TH_ERR_HIP, "AQL queue does not drain");
+            }
         }
+        hsa_queue_store_write_index_relaxed(q, idx + 1);
         hsa_kernel_dispatch_packet_t* pk = (hsa_kernel_dispatch_packet_t*)q->base_address + (idx & (q->size - 1));
         const uint16_t setup = 3 << HSA_KERNEL_DISPATCH_PACKET_SETUP_DIMENSIONS;
         pk->workgroup_size_x = p.block[0]; pk->workgroup_size_y = p.block[1]; pk->workgroup_size_z = p.block[2];
