@@ -267,6 +267,7 @@ struct AqlPacket {
 struct AqlSeq {
     th_device* dev = nullptr;
     bool write_through = false;
+    bool independent = false;  // no kernel reads what another kernel of the sequence writes
     std::vector<AqlPacket> packets;
     std::vector<char> kargs;     // host image of the kernarg segments
     char* kargs_dev = nullptr;   // device copy the packets point at
@@ -337,12 +338,13 @@ void aql_record_launch(AqlSeq* seq, const void* kernel, dim3 grid, dim3 block, s
     seq->packets.push_back(p);
 }
 
-AqlSeq* aql_record(th_device* d, bool write_through, const std::function<void()>& enqueue) {
+AqlSeq* aql_record(th_device* d, bool write_through, const std::function<void()>& enqueue, bool independent) {
     TH_REQUIRE(!g_recording, "nested AQL recording");
     aql_dev(d);
     AqlSeq* seq = new AqlSeq;
     seq->dev = d;
     seq->write_through = write_through;
+    seq->independent = independent && write_through;
     // Anything other than a kernel launch would go to the stream: capture the
     // stream meanwhile and refuse a sequence that leaves nodes in the capture.
     hipGraph_t g = nullptr;
@@ -400,7 +402,9 @@ void aql_submit(const AqlSeq& seq, size_t repeat) {
     // measured another 0.13-0.25 us per launch, but the memory model gives
     // no guarantee for plain loads then.)
     const uint16_t mid_rel = seq.write_through ? HSA_FENCE_SCOPE_NONE : HSA_FENCE_SCOPE_AGENT;
-    const uint16_t mid_acq = HSA_FENCE_SCOPE_AGENT;
+    // A sequence whose kernels read nothing another of its kernels writes
+    // needs no acquire between them either.
+    const uint16_t mid_acq = seq.independent ? HSA_FENCE_SCOPE_NONE : HSA_FENCE_SCOPE_AGENT;
     hsa_signal_add_relaxed(a->done, 1);
     a->in_flight = true;
     uint64_t idx = 0;

@@ -14,7 +14,10 @@ bool aql_enabled();
 // write_through: every kernel in it stores the values later kernels read with
 // write-through stores, so the packets carry no fences between them.
 // Anything `enqueue` puts on the stream other than a kernel is an error.
-AqlSeq* aql_record(th_device* d, bool write_through, const std::function<void()>& enqueue);
+// independent (with write_through): no kernel of the sequence reads what
+// another of its kernels writes, so the packets carry no acquire either.
+AqlSeq* aql_record(th_device* d, bool write_through, const std::function<void()>& enqueue,
+                   bool independent = false);
 // Enqueue a replay, after earlier submissions (and after the device stream's
 // work when nothing is in flight).  Call aql_wait before further stream work.
 // repeat: the sequence `repeat` times back to back as one submission

@@ -380,16 +380,18 @@ int th_bench_linear(th_device* dev, const th_buffer* x, size_t m, th_qweight* co
         // The GEMVs (q8, and q4 at m <= 16) store their output write-through:
         // no release fences between the launches.
         const bool wt = w0->bits == 8 || m <= 16;
+        // Every call reads x and its weights and writes y: no call reads what
+        // another writes (independent).
         AqlSeq* seq = aql_record(dev, wt, [&] {
             for (size_t i = 0; i < iters; i++) call(i);
-        });
+        }, true);
         AqlSeq* warm = nullptr;
         try {
             aql_submit(*seq);  // warm replay
             // then one pass over the copies in cycle order (as below)
             warm = aql_record(dev, wt, [&] {
                 for (size_t i = 0; i < n_w; i++) call(i);
-            });
+            }, true);
             aql_submit(*warm);
             aql_stamp(dev, 0);
             aql_submit(*seq);
