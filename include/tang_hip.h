@@ -189,9 +189,9 @@ int th_gemm_q4_noalloc(th_device* dev, const th_buffer* x, size_t m, const th_qw
  * last-level cache, and return the elapsed milliseconds between HIP events
  * recorded on the device stream around them.  use_graph == 1 captures the
  * calls into one HIP graph first and times its replay; use_graph == 2 records
- * them as one sequence on the library's own AQL queue (no release fences
- * between GEMV launches, q8 or q4 at m <= 16, whose outputs are stored
- * write-through) and
+ * them as one sequence on the library's own AQL queue (GEMV launches, q8 or
+ * q4 at m <= 16, store their outputs write-through and read nothing another
+ * launch writes, so the packets carry no fences between them) and
  * times its replay between device clock stamps.  Launch i reads weight
  * ws[i % n_w], and the untimed warm-up ends with one pass over ws[0..n_w) in
  * that order, so every timed launch's weights were last read n_w launches
