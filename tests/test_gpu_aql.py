@@ -129,3 +129,24 @@ def test_decode_aql_matches_hip_graph(dev, tmp_path):
     g = np.load(out)
     assert np.array_equal(g["toks"], toks)
     assert np.array_equal(g["logits"], logits)
+
+
+def test_device_steps_continue_like_generate(dev):
+    """th_llama_set_token + two th_llama_step_device calls (each one replay,
+    the token chained on the device) leave the KV cache as th_llama_generate
+    does: a one-step generate from there gives the same token and the same
+    logits, bit for bit, as an uninterrupted three-step generate."""
+    cfg = CONFIG_SMALL
+    L = capi.lib()
+    m = device_llama(dev, cfg, 7, 8, 100)
+    try:
+        ref_toks, ref_logits = device_generate(m, cfg, 1, 100, 3)
+        capi.check(L.th_llama_fill_kv_synthetic(m, 100, 8))
+        capi.check(L.th_llama_set_token(m, 1))
+        capi.check(L.th_llama_step_device(m, 100))
+        capi.check(L.th_llama_step_device(m, 101))
+        toks, logits = device_generate(m, cfg, int(ref_toks[1]), 102, 1)
+    finally:
+        L.th_llama_destroy(m)
+    assert int(toks[0]) == int(ref_toks[2])
+    assert np.array_equal(logits, ref_logits)
