@@ -14,10 +14,13 @@
 //   -> O GEMV (epilogue: +residual, tile sums of squares)
 //   -> gate/up GEMV (prologue: RMSNorm; epilogue: SwiGLU, bf16)
 //   -> down GEMV (epilogue: +residual, tile sums of squares)
-// plus the embedding and an LM-head GEMV whose epilogue takes the argmax.
-// The whole step is captured once into a HIP graph that reads the position
-// and token from device memory: one graph launch per token, no host round
-// trip.
+// plus an LM-head GEMV (epilogue: tile maxima) and the argmax, which also
+// writes the next token's embedding.  The whole step reads the position and
+// token from device memory, so it is recorded once and replayed per token
+// with no host round trip: on the library's own AQL queue (aql.cpp; every
+// kernel stores what later kernels read write-through, so the packets carry
+// no release fences), or as a HIP graph (TANG_HIP_DISPATCH=graph, or inside
+// a caller's stream capture).
 #include <algorithm>
 #include <cstdlib>
 #include <vector>
