@@ -150,7 +150,7 @@ def decode_bench(dev, steps):
         capi.check(L.th_llama_fill_kv_synthetic(h, 2048, 33))
         init_s = time.time() - t0
         ms = ctypes.c_float()
-        capi.check(L.th_llama_time_steps(h, 10, 2048, 8, ctypes.byref(ms)))  # warm (graph build)
+        capi.check(L.th_llama_time_steps(h, 10, 2048, 8, ctypes.byref(ms)))  # warm (records the step)
         capi.check(L.th_llama_fill_kv_synthetic(h, 2048, 33))
         capi.check(L.th_llama_time_steps(h, 10, 2048, steps, ctypes.byref(ms)))
         pf = prefill_7b(L, h, c)
@@ -193,7 +193,7 @@ def moe_bench(dev, T, iters, layers=2, graph=True):
     layer earlier (2 x 321 MB > 256 MB MALL).  Algorithmic bytes per call:
     every weight byte of the experts the batch routes to (+ shared experts)
     once, the router, h in, out (averaged over the layers).  `us`: the calls
-    replayed as one HIP graph (the decode loop's launch mode);
+    replayed as one HIP graph (th_capture);
     `stream_launched_us`: the same calls enqueued one by one."""
     import ctypes
     c = MOE
