@@ -413,7 +413,8 @@ def main():
     ap.add_argument("--profile-moe", type=int, default=0,
                     help="stream-launched MoE forward calls on this many tokens plus a 256 MiB copy, for counter runs")
     ap.add_argument("--profile-decode", type=int, default=0,
-                    help="kernel traces: this many 7B decode steps (the bench's launch mode) and nothing else")
+                    help="kernel traces and counters: this many 7B decode steps (the bench's launch mode), "
+                         "the 512-token prefill, then one 256 MiB copy")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="counter runs: 240 GEMV launches, then one 256 MiB device copy as the traffic calibration")
     ap.add_argument("--profile-m", type=int, default=0,
@@ -449,7 +450,10 @@ def main():
         return
     if args.profile_decode:
         d = decode_bench(dev, args.profile_decode)
-        print(json.dumps({"profile_decode": args.profile_decode, "tok_s": d["tok_s"]}))
+        a, b = dev.alloc(256 << 20, capi.U8), dev.alloc(256 << 20, capi.U8)  # traffic calibration copy
+        capi.check(capi.lib().th_buffer_copy(b.handle, a.handle))
+        dev.sync()
+        print(json.dumps({"profile_decode": args.profile_decode, "tok_s": d["tok_s"], "copy_bytes": 256 << 20}))
         return
     if args.profile_gemv:
         gemv_bench(dev, 1, 240, 0, graph="aql")  # the bench's launch mode
