@@ -415,6 +415,9 @@ def main():
     ap.add_argument("--profile-decode", type=int, default=0,
                     help="kernel traces and counters: this many 7B decode steps (the bench's launch mode), "
                          "the 512-token prefill, then one 256 MiB copy")
+    ap.add_argument("--profile-mla", type=int, default=0,
+                    help="counter runs: this many stream-launched config-5 MLA calls (8 rotating caches), "
+                         "then one 256 MiB copy")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="counter runs: 240 GEMV launches, then one 256 MiB device copy as the traffic calibration")
     ap.add_argument("--profile-m", type=int, default=0,
@@ -454,6 +457,13 @@ def main():
         capi.check(capi.lib().th_buffer_copy(b.handle, a.handle))
         dev.sync()
         print(json.dumps({"profile_decode": args.profile_decode, "tok_s": d["tok_s"], "copy_bytes": 256 << 20}))
+        return
+    if args.profile_mla:
+        mla_bench(dev, args.profile_mla)
+        a, b = dev.alloc(256 << 20, capi.U8), dev.alloc(256 << 20, capi.U8)  # traffic calibration copy
+        capi.check(capi.lib().th_buffer_copy(b.handle, a.handle))
+        dev.sync()
+        print(json.dumps({"profile_mla": args.profile_mla, "copy_bytes": 256 << 20}))
         return
     if args.profile_gemv:
         gemv_bench(dev, 1, 240, 0, graph="aql")  # the bench's launch mode
