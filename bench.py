@@ -52,6 +52,8 @@ def gemv_bench(dev, m, steps, warmup, graph="aql"):
     y = dev.alloc(m * N)
     if warmup:
         dev.bench_linear(x, m, ws, y, warmup)
+    if graph == "aql":  # the whole protocol once, untimed: the first AQL replays of a process run slow
+        dev.bench_linear(x, m, ws, y, steps, use_graph=graph)
     ms = dev.bench_linear(x, m, ws, y, steps, use_graph=graph)
     for w in ws:
         w.free()
@@ -69,6 +71,7 @@ def q8_bench(dev, steps, copies=18):
     x = dev.upload(capi.synth_normal(11, 4096, 1.0, capi.F32))
     y = dev.alloc(4096)
     dev.bench_linear(x, 1, ws, y, 48)
+    dev.bench_linear(x, 1, ws, y, steps, use_graph="aql")  # the protocol once, untimed
     ms = dev.bench_linear(x, 1, ws, y, steps, use_graph="aql")
     for w in ws:
         w.free()
@@ -318,29 +321,26 @@ def cpu_config1(threads):
     return dict(us_per_call=round(sec * 1e6, 1), cores=threads, sample="%d full calls" % calls)
 
 
-def cpu_config3(threads):
-    """Config 3 decode step on the oracle (or_llama_decode_step at position
-    2048, KV prefilled to 2048): the 7B step is timed by layers, as
-    per-layer = t(2 layers) - t(1 layer) and s/token = t(1 layer) +
-    31 per-layer (the LM head and embedding are in both samples)."""
+def cpu_config3(threads_all):
+    """Config 3 decode step on the oracle (or_llama_decode_step): the whole
+    32-layer 7B-shape model, KV prefilled to 2048, one greedy step at
+    position 2048 timed on 1 thread (the reference is serial) and one on
+    `threads_all` threads.  Each step appends its K/V row at 2048 again,
+    so both time the same work."""
     from oracle.models import CONFIG_7B, OracleLlama
-    t = {}
-    for n_layers in (1, 2):
-        cfg = dict(CONFIG_7B, n_layers=n_layers)
-        ref = OracleLlama(cfg, 3, 33, 2048)
-        best = None
-        for _ in range(2):
-            t0 = time.time()
-            ref.step(10, 2048, threads=threads)
-            dt = time.time() - t0
-            best = dt if best is None else min(best, dt)
-        t[n_layers] = best
-        del ref
-    per_layer = t[2] - t[1]
-    s_tok = t[1] + 31 * per_layer
-    return dict(s_per_token=round(s_tok, 3), cores=threads,
-                sample="one step each with 1 and 2 layers (%.2f s, %.2f s; best of 2): %.3f s per layer"
-                       % (t[1], t[2], per_layer))
+    t0 = time.time()
+    ref = OracleLlama(CONFIG_7B, 3, 33, 2048, workers=threads_all)
+    init_s = time.time() - t0
+    out = []
+    for threads in (1, threads_all):
+        t0 = time.time()
+        ref.step(10, 2048, threads=threads)
+        dt = time.time() - t0
+        out.append(dict(s_per_token=round(dt, 3), cores=threads,
+                        sample="one full 32-layer step at position 2048 (weights generated in %.0f s, untimed)"
+                               % init_s))
+    del ref
+    return out
 
 
 def cpu_config4(threads, T, sample_tokens):
@@ -371,13 +371,20 @@ def cpu_config5(threads):
 
 
 def cpu_model():
+    """The host CPU as /proc/cpuinfo names it: model name, vendor, family,
+    model and stepping of the first processor, and the logical CPU count."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break  # the first processor's block
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    return "%s (vendor %s, family %s, model %s, stepping %s; %d logical CPUs on the host)" % (
+        info.get("model name", "?"), info.get("vendor_id", "?"), info.get("cpu family", "?"), info.get("model", "?"),
+        info.get("stepping", "?"), os.cpu_count() or 0)
 
 
 def cpu_suite(threads_all):
@@ -386,7 +393,7 @@ def cpu_suite(threads_all):
     return dict(
         cpu_model=cpu_model(), nproc=os.cpu_count(), threads_used=threads_all,
         config1_q8_gemv=[cpu_config1(1), cpu_config1(threads_all)],
-        config3_decode_7b=[cpu_config3(1), cpu_config3(threads_all)],
+        config3_decode_7b=cpu_config3(threads_all),
         config4_moe=[cpu_config4(1, 16, 16), cpu_config4(threads_all, 512, 64)],
         config5_mla=[cpu_config5(1), cpu_config5(threads_all)],
     )
@@ -511,8 +518,13 @@ def main():
                                "library's AQL queue (no release fences between launches; device clock stamps)"
                                % N_COPIES,
                    "timed_launches": args.steps,
-                   "before_timing": "the sequence replayed once, then one launch per weight copy in copy order, so "
-                                    "every timed read of a copy is %d launches after its previous one" % N_COPIES,
+                   "before_timing": "the whole timed protocol run once untimed, then: one recorded sequence: 240 untimed launches (20 passes over the copies in "
+                                    "copy order), two device clock stamps back to back, one more pass, a stamp, the "
+                                    "timed launches from copy 0, a last stamp; replayed once untimed, then timed. "
+                                    "Time = last interval less the back-to-back stamps' span (one stamp kernel and "
+                                    "its dispatch), so it covers exactly the timed launches; every timed read of a "
+                                    "copy is %d launches after its previous one, and the sequence's system-scope "
+                                    "fences lie outside the stamps" % N_COPIES,
                    "stream_launched": dict(us=round(us_stream, 3), gbs=round(GEMV_BYTES[1] / us_stream / 1e3, 1)),
                    "hip_graph": dict(us=round(us_graph, 3), gbs=round(GEMV_BYTES[1] / us_graph / 1e3, 1)),
                    "M_sweep": extra},

@@ -5,6 +5,7 @@ or_llama_decode_step (crates/tang-train/examples/smollm.rs:215-300) and
 or_moe_forward (from definition).  Used by tests/ and by bench.py's CPU
 baseline leg only.
 """
+import concurrent.futures
 import ctypes
 
 import numpy as np
@@ -43,9 +44,10 @@ LINEAR_NAMES = {"wq": "self_attn.q_proj", "wk": "self_attn.k_proj", "wv": "self_
 class OracleLlama:
     """Seeded synthetic weights (as th_llama_init_synthetic), or with
     `tensors` (Llama tensor name -> f32 array) the weights a safetensors
-    file gives th_llama_load_safetensors."""
+    file gives th_llama_load_safetensors.  `workers` threads generate the
+    tensors (the result does not depend on it)."""
 
-    def __init__(self, cfg, seed, kv_seed, prefill_len, tensors=None):
+    def __init__(self, cfg, seed, kv_seed, prefill_len, tensors=None, workers=1):
         self.cfg = cfg
         c = cfg
         L, d, ff = c["n_layers"], c["d_model"], c["d_ff"]
@@ -54,14 +56,23 @@ class OracleLlama:
         views = {k: (oracle.Q4View * L)() for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd")}
         shapes = {"wq": (T_WQ, qd, d), "wk": (T_WK, kvd, d), "wv": (T_WV, kvd, d), "wo": (T_WO, d, d),
                   "wg": (T_WG, ff, d), "wu": (T_WU, ff, d), "wd": (T_WD, d, ff)}
-        for l in range(L):
-            for name, (tid, rows, cols) in shapes.items():
-                if tensors is None:
-                    nib, sc = _q4(capi.synth_seed(seed, l, tid), rows, cols)
-                else:
-                    nib, sc = _q4_from_f32(tensors["model.layers.%d.%s.weight" % (l, LINEAR_NAMES[name])], rows, cols)
-                self.keep += [nib, sc]
-                views[name][l] = oracle.Q4View(oracle.p(nib), oracle.p(sc))
+        # the seeded tensors are independent: generated in a thread pool (the
+        # generator is C code called through ctypes, which releases the GIL)
+        jobs = [(l, name) for l in range(L) for name in shapes]
+
+        def make(job):
+            l, name = job
+            tid, rows, cols = shapes[name]
+            if tensors is None:
+                return _q4(capi.synth_seed(seed, l, tid), rows, cols)
+            return _q4_from_f32(tensors["model.layers.%d.%s.weight" % (l, LINEAR_NAMES[name])], rows, cols)
+
+        with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
+            made = list(ex.map(make, jobs))
+        for (l, name), (nib, sc) in zip(jobs, made):
+            self.keep += [nib, sc]
+            views[name][l] = oracle.Q4View(oracle.p(nib), oracle.p(sc))
+        del made
         if tensors is None:
             lm_nib, lm_sc = _q4(capi.synth_seed(seed, L, T_LM_HEAD), c["vocab"], d)
             self.embed = capi.synth_normal(capi.synth_seed(seed, L, T_EMBED), c["vocab"] * d, NORM_STD, capi.BF16)
@@ -83,12 +94,15 @@ class OracleLlama:
         self.cos, self.sin = oracle.rope_tables(c["head_dim"], c["max_seq"], c["rope_theta"])
         self.kc = np.zeros((L, c["max_seq"], kvd), np.uint16)
         self.vc = np.zeros((L, c["max_seq"], kvd), np.uint16)
-        for l in range(L):
+        def fill(l):
             n = prefill_len * kvd
             self.kc[l, :prefill_len] = capi.synth_normal(capi.synth_seed(kv_seed, l, T_KCACHE), n, 1.0,
                                                          capi.F16).reshape(prefill_len, kvd)
             self.vc[l, :prefill_len] = capi.synth_normal(capi.synth_seed(kv_seed, l, T_VCACHE), n, 1.0,
                                                          capi.F16).reshape(prefill_len, kvd)
+
+        with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, workers)) as ex:
+            list(ex.map(fill, range(L)))
         self.W = oracle.LlamaWeights(
             oracle.p(self.embed), oracle.p(self.attn_norm), oracle.p(self.ffn_norm), oracle.p(self.final_norm),
             ctypes.cast(views["wq"], ctypes.c_void_p), ctypes.cast(views["wk"], ctypes.c_void_p),

@@ -67,7 +67,37 @@ constexpr double WAIT_LIMIT_S = 120.0;
 struct KernelInfo {
     uint64_t object = 0;
     uint32_t kernarg_bytes = 0, group_bytes = 0, private_bytes = 0;
+    bool write_through = false;  // listed in WRITE_THROUGH_KERNELS
 };
+
+// The kernels a write-through sequence may hold: every global store they make
+// is write-through (relaxed agent-scope atomic stores, `sc1`), so no release
+// fence is needed between them and the kernels after them.  An entry matches
+// a mangled kernel name that contains both strings (epilogue "" = any).
+// tests/test_aql_write_through.py disassembles the built library and checks
+// every store of every kernel an entry matches; aql_record_launch refuses a
+// kernel no entry matches in a write-through sequence.
+struct WriteThroughKernel {
+    const char* kernel;
+    const char* epilogue;
+};
+const WriteThroughKernel WRITE_THROUGH_KERNELS[] = {
+    {"q4_gemv_kernel", "EpiStore"},
+    {"q4_gemv_kernel", "EpiQKV"},
+    {"q4_gemv_kernel", "EpiAddToSsq"},
+    {"q4_gemv_kernel", "EpiSwiGLU"},
+    {"q4_gemv_kernel", "EpiTileMax"},
+    {"q8_gemv_kernel", "EpiStore"},
+    {"attn_decode_kernel", ""},
+    {"llama_argmax_embed_kernel", ""},
+    {"aql_stamp_kernel", ""},
+};
+
+bool is_write_through_kernel(const std::string& mangled) {
+    for (const WriteThroughKernel& w : WRITE_THROUGH_KERNELS)
+        if (mangled.find(w.kernel) != std::string::npos && mangled.find(w.epilogue) != std::string::npos) return true;
+    return false;
+}
 
 // Per-process: the code objects of this library, loaded once per agent.
 struct Program {
@@ -185,6 +215,7 @@ hsa_status_t collect_kernel(hsa_executable_t, hsa_agent_t, hsa_executable_symbol
     (void)hsa_executable_symbol_get_info(s, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_KERNARG_SEGMENT_SIZE, &k.kernarg_bytes);
     (void)hsa_executable_symbol_get_info(s, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_GROUP_SEGMENT_SIZE, &k.group_bytes);
     (void)hsa_executable_symbol_get_info(s, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_PRIVATE_SEGMENT_SIZE, &k.private_bytes);
+    k.write_through = is_write_through_kernel(name);
     ((SymCtx*)data)->prog->by_name.emplace(name, k);
     return HSA_STATUS_SUCCESS;
 }
@@ -251,7 +282,7 @@ struct AqlDev {
     hsa_queue_t* queue = nullptr;
     hsa_signal_t done{};
     std::atomic<int> error{0};
-    unsigned long long* stamps = nullptr;  // device: two clock stamps
+    unsigned long long* stamps = nullptr;  // device: four clock stamps
     AqlSeq* stamp_seq[2] = {nullptr, nullptr};
     bool in_flight = false;
 };
@@ -294,7 +325,7 @@ static AqlDev* aql_dev(th_device* d) {
         TH_HSA(hsa_queue_create(agent, QUEUE_PACKETS, HSA_QUEUE_TYPE_SINGLE, queue_error, &a->error, UINT32_MAX,
                                 UINT32_MAX, &a->queue));
         TH_HSA(hsa_signal_create(0, 0, nullptr, &a->done));
-        TH_HIP(hipMalloc((void**)&a->stamps, 2 * sizeof(unsigned long long)));
+        TH_HIP(hipMalloc((void**)&a->stamps, 4 * sizeof(unsigned long long)));
     } catch (...) {
         if (a->queue) (void)hsa_queue_destroy(a->queue);
         delete a;
@@ -308,6 +339,12 @@ void aql_record_launch(AqlSeq* seq, const void* kernel, dim3 grid, dim3 block, s
                        size_t bytes) {
     AqlDev* a = aql_dev(seq->dev);
     const KernelInfo k = kernel_info(a->prog, kernel);
+    if (seq->write_through && !k.write_through) {
+        Dl_info di{};
+        const char* name = dladdr(kernel, &di) && di.dli_sname ? di.dli_sname : "?";
+        throw Error(TH_ERR_INVALID, std::string("kernel in a write-through sequence is not a write-through kernel: ") +
+                                        name);
+    }
     const size_t explicit_end = round_up(bytes, 8);
     size_t seg = std::max<size_t>(k.kernarg_bytes, bytes);
     const bool hidden = k.kernarg_bytes > explicit_end;
@@ -469,10 +506,23 @@ void aql_stamp(th_device* d, int which) {
     aql_submit(*a->stamp_seq[which]);
 }
 
+void aql_stamp_launch(th_device* d, int which) {
+    TH_REQUIRE(which >= 0 && which < 4, "stamp slot out of range");
+    AqlDev* a = aql_dev(d);
+    TH_LAUNCH(aql_stamp_kernel, dim3(1), dim3(64), 0, d->stream, a->stamps + which);
+}
+
 float aql_stamped_ms(th_device* d) {
     aql_wait(d);
     unsigned long long t[2];
     TH_HIP(hipMemcpy(t, d->aql->stamps, sizeof t, hipMemcpyDeviceToHost));
+    return (float)((double)(t[1] - t[0]) / 100e6 * 1e3);
+}
+
+float aql_stamp_span_ms(th_device* d) {
+    aql_wait(d);
+    unsigned long long t[2];
+    TH_HIP(hipMemcpy(t, d->aql->stamps + 2, sizeof t, hipMemcpyDeviceToHost));
     return (float)((double)(t[1] - t[0]) / 100e6 * 1e3);
 }
 

@@ -29,6 +29,11 @@ void aql_free(AqlSeq* seq);
 // Device clock stamps around submitted work: aql_stamp(d, 0), submissions,
 // aql_stamp(d, 1), then aql_stamped_ms(d) waits and returns the interval.
 void aql_stamp(th_device* d, int which);
+// The stamp kernel launched on the device stream (which < 4), so that a
+// sequence being recorded can carry its own stamps: aql_stamped_ms reads
+// stamps 0 and 1, aql_stamp_span_ms stamps 2 and 3 (after waiting).
+void aql_stamp_launch(th_device* d, int which);
+float aql_stamp_span_ms(th_device* d);
 float aql_stamped_ms(th_device* d);
 
 // Device stream and AQL queue both drained.

@@ -382,27 +382,34 @@ int th_bench_linear(th_device* dev, const th_buffer* x, size_t m, th_qweight* co
         const bool wt = w0->bits == 8 || m <= 16;
         // Every call reads x and its weights and writes y: no call reads what
         // another writes (independent).
+        // One sequence: whole passes over the copies (at least 240 launches,
+        // so the timed launches run in the steady state of a busy queue and
+        // every copy was last read n_w launches earlier), two clock stamps
+        // back to back (the span of a stamp kernel and its dispatch), one
+        // more pass, a clock stamp, the `iters` timed launches from copy 0,
+        // a last stamp.  The time is the last interval less the stamps' own
+        // span.  The sequence's system-scope acquire and release sit on its
+        // first and last packets, outside both intervals.  It is replayed
+        // twice; the second replay is timed.
+        const size_t pre = ceil_div(std::max<size_t>(240, n_w), n_w) * n_w;
         AqlSeq* seq = aql_record(dev, wt, [&] {
+            for (size_t i = 0; i < pre; i++) call(i);
+            aql_stamp_launch(dev, 2);
+            aql_stamp_launch(dev, 3);
+            for (size_t i = 0; i < n_w; i++) call(i);
+            aql_stamp_launch(dev, 0);
             for (size_t i = 0; i < iters; i++) call(i);
+            aql_stamp_launch(dev, 1);
         }, true);
-        AqlSeq* warm = nullptr;
         try {
             aql_submit(*seq);  // warm replay
-            // then one pass over the copies in cycle order (as below)
-            warm = aql_record(dev, wt, [&] {
-                for (size_t i = 0; i < n_w; i++) call(i);
-            }, true);
-            aql_submit(*warm);
-            aql_stamp(dev, 0);
+            aql_wait(dev);
             aql_submit(*seq);
-            aql_stamp(dev, 1);
-            *ms = aql_stamped_ms(dev);
+            *ms = aql_stamped_ms(dev) - aql_stamp_span_ms(dev);
         } catch (...) {
-            aql_free(warm);
             aql_free(seq);
             throw;
         }
-        aql_free(warm);
         aql_free(seq);
     } else if (use_graph) {
         hipGraph_t g;

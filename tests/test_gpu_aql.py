@@ -14,7 +14,7 @@ import sys
 import numpy as np
 import pytest
 
-from llama_ref import CONFIG_SMALL, device_generate, device_llama
+from llama_ref import CONFIG_7B, CONFIG_SMALL, device_generate, device_llama
 from tang_amd import capi
 
 pytestmark = pytest.mark.gpu
@@ -96,15 +96,29 @@ def test_q8_gemv_aql_chain_matches_stream(dev):
 _CHILD = r"""
 import sys, numpy as np
 sys.path.insert(0, {here!r}); sys.path.insert(0, {root!r})
-from llama_ref import CONFIG_SMALL, device_generate, device_llama
+from llama_ref import CONFIG_7B, CONFIG_SMALL, device_generate, device_llama
 from tang_amd import capi
+cfg = {cfg}
 dev = capi.HipComputeDevice(0)
-m = device_llama(dev, CONFIG_SMALL, 7, 8, 100)
-toks, logits = device_generate(m, CONFIG_SMALL, 1, 100, 48)
+m = device_llama(dev, cfg, {seed}, {kv_seed}, {prefill})
+toks, logits = device_generate(m, cfg, {token}, {prefill}, {steps})
 capi.lib().th_llama_destroy(m)
 dev.close()
 np.savez({out!r}, toks=toks, logits=logits)
 """
+
+
+def _graph_replay_child(tmp_path, cfg_name, seed, kv_seed, prefill, token, steps, timeout):
+    """The same generation in a child process with TANG_HIP_DISPATCH=graph
+    (HIP graph replay, with the fences HIP puts between graph nodes)."""
+    out = str(tmp_path / "graph.npz")
+    env = dict(os.environ, TANG_HIP_DISPATCH="graph")
+    code = _CHILD.format(here=HERE, root=os.path.dirname(HERE), out=out, cfg=cfg_name, seed=seed, kv_seed=kv_seed,
+                         prefill=prefill, token=token, steps=steps)
+    print("child: graph dispatch, %s, %d steps" % (cfg_name, steps), flush=True)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return np.load(out)
 
 
 def test_decode_aql_matches_hip_graph(dev, tmp_path):
@@ -120,13 +134,24 @@ def test_decode_aql_matches_hip_graph(dev, tmp_path):
         assert 0 < ms.value < 1e4
     finally:
         capi.lib().th_llama_destroy(m)
-    out = str(tmp_path / "graph.npz")
-    env = dict(os.environ, TANG_HIP_DISPATCH="graph")
-    code = _CHILD.format(here=HERE, root=os.path.dirname(HERE), out=out)
-    print("child: graph dispatch", flush=True)
-    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=100)
-    assert r.returncode == 0, r.stderr[-2000:]
-    g = np.load(out)
+    g = _graph_replay_child(tmp_path, "CONFIG_SMALL", 7, 8, 100, 1, 48, 100)
+    assert np.array_equal(g["toks"], toks)
+    assert np.array_equal(g["logits"], logits)
+
+
+def test_decode_7b_aql_matches_hip_graph(dev, tmp_path):
+    """The 7B shape (config 3: 161 write-through kernels per step, attention
+    split over every CU, workgroups on all eight XCDs), 6 greedy steps from
+    position 2048: the AQL replay's tokens and final logits equal the HIP
+    graph replay's bit for bit, so no kernel of the step reads a value
+    another XCD left in its own L2."""
+    cfg = CONFIG_7B
+    m = device_llama(dev, cfg, 3, 33, 2048)
+    try:
+        toks, logits = device_generate(m, cfg, 10, 2048, 6)
+    finally:
+        capi.lib().th_llama_destroy(m)
+    g = _graph_replay_child(tmp_path, "CONFIG_7B", 3, 33, 2048, 10, 6, 110)
     assert np.array_equal(g["toks"], toks)
     assert np.array_equal(g["logits"], logits)
 
