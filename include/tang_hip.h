@@ -228,9 +228,40 @@ int th_bias_add(th_device* dev, const th_buffer* matrix, const th_buffer* bias, 
 /* ComputeDevice::add_assign (device.rs:767; cpu.rs:650): dst += src, equal lengths. */
 int th_add_assign(th_device* dev, th_buffer* dst, const th_buffer* src);
 
-/* Run-time compiled element-wise kernels: the source tang-expr generates for
- * ComputeDevice::elementwise (device.rs:93; the CUDA backend's path is
- * cuda.rs:1135-1190), i.e. a kernel
+/* ComputeDevice::elementwise (device.rs:93; the CPU backend's semantics,
+ * cpu.rs:68-97): the closure's tang-expr graph (trace(), tang-expr/src/lib.rs:61)
+ * is handed over as its nodes in graph order (node.rs:58-90), operands
+ * indexing earlier nodes.  The library generates the HIP kernel, compiles it
+ * for gfx950 once per distinct graph (hiprtc, cached per device) and runs it
+ * over numel elements: out[i] = f(in0[i], ..., in{n-1}[i]), each input widened
+ * to f64, every node evaluated in f64, the result rounded to f32 once.
+ * th_expr_source returns the generated source (len = its length; up to cap-1
+ * bytes and a NUL are written to buf when buf is not NULL). */
+enum {
+    TH_EXPR_VAR = 0,  /* input a */
+    TH_EXPR_LIT = 1,  /* the value lit */
+    TH_EXPR_ADD = 2,  /* a + b */
+    TH_EXPR_MUL = 3,  /* a * b */
+    TH_EXPR_NEG = 4,  /* -a */
+    TH_EXPR_RECIP = 5, /* 1 / a */
+    TH_EXPR_SQRT = 6,
+    TH_EXPR_SIN = 7,
+    TH_EXPR_ATAN2 = 8, /* atan2(a = y, b = x) */
+    TH_EXPR_EXP2 = 9,
+    TH_EXPR_LOG2 = 10,
+    TH_EXPR_SELECT = 11 /* a > 0 ? b : c */
+};
+typedef struct th_expr_node {
+    uint32_t op;      /* TH_EXPR_* */
+    uint32_t a, b, c; /* operand node indices; TH_EXPR_VAR: a = input index */
+    double lit;       /* TH_EXPR_LIT */
+} th_expr_node;
+int th_expr_source(const th_expr_node* nodes, size_t n_nodes, uint32_t output, size_t n_inputs, char* buf,
+                   size_t cap, size_t* len);
+int th_elementwise_expr(th_device* dev, const th_expr_node* nodes, size_t n_nodes, uint32_t output,
+                        const th_buffer* const* inputs, size_t n_inputs, size_t numel, th_buffer* out);
+
+/* Run-time compiled kernels from HIP source: a kernel
  *   extern "C" __global__ void <entry>(const float* in0, ..., float* outputs,
  *                                      const unsigned int count)
  * with one thread per element, compiled for gfx950 with hiprtc and loaded as a

@@ -336,3 +336,47 @@ def bias_add(m, bias, numel, dim):
     out = np.empty(numel, np.float32)
     lib().or_bias_add(p(m), p(bias), numel, dim, p(out))
     return out
+
+
+def expr_eval(nodes, output, inputs):
+    """CpuDevice::elementwise (crates/tang-compute/src/cpu.rs:68-97) over a
+    graph given as th_expr_node records: every input widened to f64, each
+    live node evaluated in f64 as tang-expr's compiled closure does
+    (crates/tang-expr/src/compile.rs:99-118; Select takes `a` when the
+    condition is > 0, NaN included as false), the result rounded to f32.
+    Numpy's f64 sin/arctan2/exp2/log2 stand for Rust's (the platform libm)."""
+    ops = {0: "var", 1: "lit", 2: "add", 3: "mul", 4: "neg", 5: "recip", 6: "sqrt", 7: "sin", 8: "atan2",
+           9: "exp2", 10: "log2", 11: "select"}
+    xs = [np.asarray(v, np.float32).astype(np.float64) for v in inputs]
+    vals = {}
+    with np.errstate(all="ignore"):
+        for i in range(output + 1):
+            n = nodes[i]
+            op, a, b, c = ops[int(n["op"])], int(n["a"]), int(n["b"]), int(n["c"])
+            if op == "var":
+                v = xs[a]
+            elif op == "lit":
+                v = np.float64(n["lit"])
+            elif op == "add":
+                v = vals[a] + vals[b]
+            elif op == "mul":
+                v = vals[a] * vals[b]
+            elif op == "neg":
+                v = -vals[a]
+            elif op == "recip":
+                v = 1.0 / vals[a]
+            elif op == "sqrt":
+                v = np.sqrt(vals[a])
+            elif op == "sin":
+                v = np.sin(vals[a])
+            elif op == "atan2":
+                v = np.arctan2(vals[a], vals[b])
+            elif op == "exp2":
+                v = np.exp2(vals[a])
+            elif op == "log2":
+                v = np.log2(vals[a])
+            else:
+                v = np.where(vals[a] > 0.0, vals[b], vals[c])
+            vals[i] = v
+    n = len(xs[0]) if xs else 1
+    return np.broadcast_to(np.asarray(vals[output], np.float64), (n,)).astype(np.float32)

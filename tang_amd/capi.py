@@ -123,6 +123,8 @@ SIGNATURES = {
     "th_reduce_sum": ([_P, _P, _P, _S, _S, _I, _P], _I),
     "th_bias_add": ([_P, _P, _P, _S, _S, _P], _I),
     "th_add_assign": ([_P, _P, _P], _I),
+    "th_expr_source": ([_P, _S, ctypes.c_uint32, _S, _P, _S, _P], _I),
+    "th_elementwise_expr": ([_P, _P, _S, ctypes.c_uint32, _P, _S, _S, _P], _I),
     "th_kernel_compile": ([_P, ctypes.c_char_p, ctypes.c_char_p, _P], _I),
     "th_kernel_free": ([_P], _I),
     "th_elementwise": ([_P, _P, _S, _S, _P], _I),
@@ -133,6 +135,79 @@ SIGNATURES = {
 }
 
 _lib = None
+
+# th_expr_node (include/tang_hip.h): op, three operand indices, a literal.
+EXPR_NODE = np.dtype([("op", "<u4"), ("a", "<u4"), ("b", "<u4"), ("c", "<u4"), ("lit", "<f8")], align=True)
+(EXPR_VAR, EXPR_LIT, EXPR_ADD, EXPR_MUL, EXPR_NEG, EXPR_RECIP, EXPR_SQRT, EXPR_SIN, EXPR_ATAN2, EXPR_EXP2, EXPR_LOG2,
+ EXPR_SELECT) = range(12)
+
+
+class ExprGraph:
+    """A tang-expr expression graph (crates/tang-expr/src/graph.rs:12-143) in
+    the form th_elementwise_expr takes: nodes in creation order, identical
+    nodes shared (hash-consed), the literals 0, 1 and 2 at indices 0-2.  The
+    builder methods return node indices."""
+
+    def __init__(self):
+        self.nodes = []
+        self._index = {}
+        for v in (0.0, 1.0, 2.0):
+            self.lit(v)
+
+    def _node(self, op, a=0, b=0, c=0, lit=0.0):
+        key = (op, a, b, c, np.float64(lit).tobytes())
+        if key not in self._index:
+            self._index[key] = len(self.nodes)
+            self.nodes.append((op, a, b, c, lit))
+        return self._index[key]
+
+    def var(self, i):
+        return self._node(EXPR_VAR, i)
+
+    def lit(self, v):
+        return self._node(EXPR_LIT, lit=float(v))
+
+    def add(self, a, b):
+        return self._node(EXPR_ADD, a, b)
+
+    def mul(self, a, b):
+        return self._node(EXPR_MUL, a, b)
+
+    def neg(self, a):
+        return self._node(EXPR_NEG, a)
+
+    def recip(self, a):
+        return self._node(EXPR_RECIP, a)
+
+    def sqrt(self, a):
+        return self._node(EXPR_SQRT, a)
+
+    def sin(self, a):
+        return self._node(EXPR_SIN, a)
+
+    def atan2(self, y, x):
+        return self._node(EXPR_ATAN2, y, x)
+
+    def exp2(self, a):
+        return self._node(EXPR_EXP2, a)
+
+    def log2(self, a):
+        return self._node(EXPR_LOG2, a)
+
+    def select(self, cond, a, b):
+        return self._node(EXPR_SELECT, cond, a, b)
+
+    def array(self):
+        return np.array(self.nodes, EXPR_NODE)
+
+    def source(self, output, n_inputs):
+        """The HIP source th_elementwise_expr generates for this graph."""
+        nodes = self.array()
+        n = ctypes.c_size_t()
+        check(lib().th_expr_source(ptr(nodes), len(nodes), output, n_inputs, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value + 1)
+        check(lib().th_expr_source(ptr(nodes), len(nodes), output, n_inputs, buf, n.value + 1, ctypes.byref(n)))
+        return buf.value.decode()
 
 
 def lib():
@@ -597,12 +672,26 @@ class HipComputeDevice:
     def add_assign(self, dst, src):
         check(lib().th_add_assign(self.handle, dst.handle, src.handle))
 
+    def elementwise(self, inputs, numel, f):
+        """ComputeDevice::elementwise (device.rs:93): f(graph, vars) builds the
+        output node from one variable per input buffer, as the reference's
+        closure does under trace()."""
+        g = ExprGraph()
+        out_id = f(g, [g.var(i) for i in range(len(inputs))])
+        nodes = g.array()
+        out = self.alloc(numel)
+        arr = (ctypes.c_void_p * max(len(inputs), 1))(*[b.handle for b in inputs])
+        check(lib().th_elementwise_expr(self.handle, ptr(nodes), len(nodes), out_id, arr, len(inputs), numel,
+                                        out.handle))
+        return out
+
     def compile_kernel(self, source, entry="k0"):
         h = ctypes.c_void_p()
         check(lib().th_kernel_compile(self.handle, source.encode(), entry.encode(), ctypes.byref(h)))
         return h
 
-    def elementwise(self, kernel, inputs, numel):
+    def run_kernel(self, kernel, inputs, numel):
+        """A kernel from compile_kernel over numel elements (th_elementwise)."""
         out = self.alloc(numel)
         arr = (ctypes.c_void_p * max(len(inputs), 1))(*[b.handle for b in inputs])
         check(lib().th_elementwise(kernel, arr, len(inputs), numel, out.handle))

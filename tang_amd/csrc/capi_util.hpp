@@ -44,6 +44,8 @@ int* device_counters(th_device* dev, size_t n);
 // GEMM call (may be held at the same time as device_scratch).
 void* device_scratch_x(th_device* dev, size_t bytes);
 void require_len(const th_buffer* b, th_dtype dt, size_t n, const char* what);
+// Unloads the device's compiled element-wise graphs (expr.cpp).
+void expr_release(th_device* d);
 void require_len_any(const th_buffer* b, size_t n, const char* what);
 
 th_qweight* q4_pack(th_device* dev, const uint8_t* nib, const void* scales, th_dtype sdt, size_t rows,

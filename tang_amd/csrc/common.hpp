@@ -116,6 +116,7 @@ inline uint16_t f32_to_f16_host(float v) { return __builtin_bit_cast(uint16_t, (
 
 namespace th {
 struct AqlDev;
+struct ExprCache;
 void aql_wait(th_device* d);
 void aql_release(th_device* d);
 }  // namespace th
@@ -135,6 +136,7 @@ struct th_device {
     int live = 0;          // buffers, weights and engines that hold this device
     bool closed = false;   // th_device_destroy ran; the struct waits for live == 0
     th::AqlDev* aql = nullptr;  // HSA queue for recorded sequences (created on first use)
+    th::ExprCache* expr = nullptr;  // compiled element-wise graphs (expr.cpp), by source
 };
 
 // Objects holding a th_device keep the struct alive: th_device_destroy

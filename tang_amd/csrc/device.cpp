@@ -269,6 +269,7 @@ int th_device_destroy(th_device* d) {
     TH_REQUIRE(!d->closed, "device already destroyed");
     th::aql_release(d);
     (void)hipStreamSynchronize(d->stream);
+    th::expr_release(d);
     if (d->scratch) (void)hipFree(d->scratch);
     if (d->scratch_x) (void)hipFree(d->scratch_x);
     if (d->counters) (void)hipFree(d->counters);

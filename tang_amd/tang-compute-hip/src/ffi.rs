@@ -114,6 +114,32 @@ pub struct th_sampling_config {
     pub max_tokens: usize,
 }
 
+// th_expr_node.op: the tang-expr node kinds (crates/tang-expr/src/node.rs:58-90)
+pub const TH_EXPR_VAR: u32 = 0;
+pub const TH_EXPR_LIT: u32 = 1;
+pub const TH_EXPR_ADD: u32 = 2;
+pub const TH_EXPR_MUL: u32 = 3;
+pub const TH_EXPR_NEG: u32 = 4;
+pub const TH_EXPR_RECIP: u32 = 5;
+pub const TH_EXPR_SQRT: u32 = 6;
+pub const TH_EXPR_SIN: u32 = 7;
+pub const TH_EXPR_ATAN2: u32 = 8;
+pub const TH_EXPR_EXP2: u32 = 9;
+pub const TH_EXPR_LOG2: u32 = 10;
+pub const TH_EXPR_SELECT: u32 = 11;
+
+/// One node of an expression graph: operands are indices of earlier nodes
+/// (`Var`: `a` is the input index; `Lit`: the value is `lit`).
+#[repr(C)]
+#[derive(Clone, Copy)]
+pub struct th_expr_node {
+    pub op: u32,
+    pub a: u32,
+    pub b: u32,
+    pub c: u32,
+    pub lit: f64,
+}
+
 #[link(name = "tang_hip")]
 extern "C" {
     pub fn th_last_error() -> *const c_char;
@@ -165,6 +191,8 @@ extern "C" {
     pub fn th_reduce_sum(dev: *mut th_device, in_: *const th_buffer, shape: *const usize, ndim: usize, axis: usize, accumulate: c_int, out: *mut th_buffer) -> c_int;
     pub fn th_bias_add(dev: *mut th_device, matrix: *const th_buffer, bias: *const th_buffer, numel: usize, dim: usize, out: *mut th_buffer) -> c_int;
     pub fn th_add_assign(dev: *mut th_device, dst: *mut th_buffer, src: *const th_buffer) -> c_int;
+    pub fn th_expr_source(nodes: *const th_expr_node, n_nodes: usize, output: u32, n_inputs: usize, buf: *mut c_char, cap: usize, len: *mut usize) -> c_int;
+    pub fn th_elementwise_expr(dev: *mut th_device, nodes: *const th_expr_node, n_nodes: usize, output: u32, inputs: *const *const th_buffer, n_inputs: usize, numel: usize, out: *mut th_buffer) -> c_int;
     pub fn th_kernel_compile(dev: *mut th_device, source: *const c_char, entry: *const c_char, out: *mut *mut th_kernel) -> c_int;
     pub fn th_kernel_free(k: *mut th_kernel) -> c_int;
     pub fn th_elementwise(k: *mut th_kernel, inputs: *const *const th_buffer, n_inputs: usize, numel: usize, out: *mut th_buffer) -> c_int;

@@ -8,12 +8,15 @@
 //! synchronisation points (device.rs:75, :367).  The quantized decode path the
 //! reference runs on the CPU (`q4_matvec` / `q8_matvec`,
 //! crates/tang-infer/src/quantize.rs:227-289) is the `QuantizedCompute`
-//! extension trait below, plus MoE, MLA and a whole-model decode engine.
+//! extension trait below; `LatentAttention` adds MLA decode, `HipMoe` a MoE
+//! layer, and `HipLlama` the device-resident decode engine whose `generate`
+//! replaces `tang_infer::generate` (crates/tang-infer/src/sampling.rs:229-256)
+//! for a Llama-shaped model.
 //!
 //! Errors panic with the library's message, as the reference backends do
 //! (e.g. crates/tang-compute/src/cuda.rs:385).  Like `CudaComputeDevice`, the
-//! device is `Send` but not `Sync` (one device per thread; the element-wise
-//! kernel cache is a `RefCell`).
+//! device is `Send` but not `Sync` (one device per thread).  The engines
+//! borrow the device they run on, so it outlives them.
 //!
 //! Training-only operators (the backward passes, cross-entropy, AdamW) are
 //! outside this backend, which serves the inference path: they panic with
@@ -22,17 +25,18 @@
 
 pub mod ffi;
 
-use std::cell::RefCell;
-use std::collections::HashMap;
 use std::ffi::{CStr, CString};
+use std::marker::PhantomData;
+use std::path::Path;
 use std::os::raw::{c_int, c_void};
 use std::ptr;
 
 use tang_compute::{ComputeBuffer, ComputeDevice};
 use tang_expr::codegen::Dialect;
-use tang_expr::node::ExprId;
+use tang_expr::node::{ExprId, Node};
 use tang_expr::trace;
 use tang_infer::quantize::{QuantizedQ4, QuantizedQ8};
+use tang_infer::SamplingConfig;
 
 fn last_error() -> String {
     unsafe { CStr::from_ptr(ffi::th_last_error()).to_string_lossy().into_owned() }
@@ -105,21 +109,9 @@ impl ComputeBuffer for HipBuffer {
 // Device
 // ---------------------------------------------------------------------------
 
-struct Kernel(*mut ffi::th_kernel);
-
-impl Drop for Kernel {
-    fn drop(&mut self) {
-        unsafe {
-            ffi::th_kernel_free(self.0);
-        }
-    }
-}
-
 /// One MI355X (HIP device ordinal) with one stream.
 pub struct HipComputeDevice {
     dev: *mut ffi::th_device,
-    /// Element-wise kernels compiled by hiprtc, keyed by their source.
-    kernels: RefCell<HashMap<String, Kernel>>,
 }
 
 unsafe impl Send for HipComputeDevice {}
@@ -129,7 +121,7 @@ impl HipComputeDevice {
     pub fn new(ordinal: usize) -> Self {
         let mut dev = ptr::null_mut();
         check(unsafe { ffi::th_device_create(ordinal as c_int, &mut dev) });
-        HipComputeDevice { dev, kernels: RefCell::new(HashMap::new()) }
+        HipComputeDevice { dev }
     }
 
     pub fn raw(&self) -> *mut ffi::th_device {
@@ -148,18 +140,6 @@ impl HipComputeDevice {
         b
     }
 
-    fn compiled(&self, source: &str, entry: &str) -> *mut ffi::th_kernel {
-        if let Some(k) = self.kernels.borrow().get(source) {
-            return k.0;
-        }
-        let src = CString::new(source).expect("kernel source holds a NUL byte");
-        let name = CString::new(entry).expect("entry name holds a NUL byte");
-        let mut k = ptr::null_mut();
-        check(unsafe { ffi::th_kernel_compile(self.dev, src.as_ptr(), name.as_ptr(), &mut k) });
-        self.kernels.borrow_mut().insert(source.to_string(), Kernel(k));
-        k
-    }
-
     fn matmul_ex(&self, a: &HipBuffer, b: &HipBuffer, c: &mut HipBuffer, m: usize, k: usize, n: usize, ta: bool,
                  tb: bool, accumulate: bool) {
         check(unsafe {
@@ -170,11 +150,31 @@ impl HipComputeDevice {
 
 impl Drop for HipComputeDevice {
     fn drop(&mut self) {
-        self.kernels.borrow_mut().clear();
         // buffers still alive keep the library's device state until they drop
         unsafe {
             ffi::th_device_destroy(self.dev);
         }
+    }
+}
+
+/// A tang-expr node (node.rs:58-90) as the C ABI's `th_expr_node`.
+fn expr_node(n: &Node) -> ffi::th_expr_node {
+    let mk = |op: u32, a: ExprId, b: ExprId, c: ExprId| ffi::th_expr_node { op, a: a.index(), b: b.index(),
+                                                                            c: c.index(), lit: 0.0 };
+    let z = ExprId::ZERO;
+    match *n {
+        Node::Var(i) => ffi::th_expr_node { op: ffi::TH_EXPR_VAR, a: i as u32, b: 0, c: 0, lit: 0.0 },
+        Node::Lit(bits) => ffi::th_expr_node { op: ffi::TH_EXPR_LIT, a: 0, b: 0, c: 0, lit: f64::from_bits(bits) },
+        Node::Add(a, b) => mk(ffi::TH_EXPR_ADD, a, b, z),
+        Node::Mul(a, b) => mk(ffi::TH_EXPR_MUL, a, b, z),
+        Node::Neg(a) => mk(ffi::TH_EXPR_NEG, a, z, z),
+        Node::Recip(a) => mk(ffi::TH_EXPR_RECIP, a, z, z),
+        Node::Sqrt(a) => mk(ffi::TH_EXPR_SQRT, a, z, z),
+        Node::Sin(a) => mk(ffi::TH_EXPR_SIN, a, z, z),
+        Node::Atan2(y, x) => mk(ffi::TH_EXPR_ATAN2, y, x, z),
+        Node::Exp2(a) => mk(ffi::TH_EXPR_EXP2, a, z, z),
+        Node::Log2(a) => mk(ffi::TH_EXPR_LOG2, a, z, z),
+        Node::Select(c, a, b) => mk(ffi::TH_EXPR_SELECT, c, a, b),
     }
 }
 
@@ -189,11 +189,13 @@ fn training_only(op: &str) -> ! {
 impl ComputeDevice for HipComputeDevice {
     type Buffer = HipBuffer;
 
-    /// Element-wise kernels are generated as tang-expr's CUDA-dialect C
-    /// (`extern "C" __global__`, blockIdx/threadIdx, libm names), which hiprtc
-    /// compiles for gfx950 as it stands.
+    /// No `Dialect` variant names HIP, and this device consumes no shader
+    /// text: `elementwise` hands the traced `ExprGraph` itself to the library,
+    /// which generates gfx950 code for it.  `C` is reported because the
+    /// device evaluates a graph as the C / CPU path does (f64 per node, one
+    /// rounding to f32 at the end).
     fn dialect(&self) -> Dialect {
-        Dialect::Cuda
+        Dialect::C
     }
 
     fn total_memory_bytes(&self) -> usize {
@@ -255,19 +257,25 @@ impl ComputeDevice for HipComputeDevice {
         }
     }
 
-    // -- element-wise via tang-expr (device.rs:93; the CUDA path is cuda.rs:1135-1190) --
+    // -- element-wise via tang-expr (device.rs:93; the CPU semantics cpu.rs:68-97) --
 
+    /// Traces the closure as every backend does (`trace`, tang-expr/src/lib.rs:61)
+    /// and passes the graph's nodes, in graph order, to `th_elementwise_expr`:
+    /// the library generates the HIP kernel from them, compiles it once per
+    /// distinct graph and runs it.
     fn elementwise(&self, inputs: &[&HipBuffer], numel: usize, f: &dyn Fn(&[ExprId]) -> ExprId) -> HipBuffer {
         let n_inputs = inputs.len();
         let (graph, output) = trace(|| {
             let vars: Vec<ExprId> = (0..n_inputs as u16).map(ExprId::var).collect();
             f(&vars)
         });
-        let kernel = graph.to_kernel(&[output], n_inputs, Dialect::Cuda);
-        let k = self.compiled(&kernel.source, kernel.entry_point);
+        let nodes: Vec<ffi::th_expr_node> = graph.nodes_slice().iter().map(expr_node).collect();
         let raw: Vec<*const ffi::th_buffer> = inputs.iter().map(|b| b.raw as *const ffi::th_buffer).collect();
         let out = self.buffer(ffi::TH_F32, numel);
-        check(unsafe { ffi::th_elementwise(k, raw.as_ptr(), n_inputs, numel, out.raw) });
+        check(unsafe {
+            ffi::th_elementwise_expr(self.dev, nodes.as_ptr(), nodes.len(), output.index(), raw.as_ptr(), n_inputs,
+                                     numel, out.raw)
+        });
         out
     }
 
@@ -558,5 +566,263 @@ impl QuantizedCompute for HipComputeDevice {
             check(unsafe { ffi::th_gemv_q8(self.dev, x.raw, m, w.raw, y.raw) });
         }
         y
+    }
+}
+
+impl HipComputeDevice {
+    /// A copy of `src` in another element type (`ffi::TH_F32`, `TH_BF16`,
+    /// `TH_F16`): f32 -> bf16 rounds as crates/tang-compute/src/cuda.rs:22-27.
+    pub fn convert(&self, src: &HipBuffer, dtype: c_int) -> HipBuffer {
+        let out = self.buffer(dtype, src.len);
+        check(unsafe { ffi::th_convert(self.dev, src.raw, out.raw) });
+        out
+    }
+
+    /// An int8 matrix with one f32 scale per row (the MLA projections of
+    /// BASELINE config 5): `q` is `[rows][cols]` row-major.
+    pub fn upload_q8_rowwise(&self, q: &[i8], row_scale: &[f32], rows: usize, cols: usize) -> HipQWeight {
+        assert_eq!(q.len(), rows * cols, "q must be [rows][cols]");
+        assert_eq!(row_scale.len(), rows, "one scale per row");
+        let mut raw = ptr::null_mut();
+        check(unsafe { ffi::th_q8_upload_rowwise(self.dev, q.as_ptr(), row_scale.as_ptr(), rows, cols, &mut raw) });
+        HipQWeight { raw, rows, cols, bits: 8 }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MLA decode (no counterpart in the reference)
+// ---------------------------------------------------------------------------
+
+/// Absorbed multi-head latent attention for one decode position per
+/// sequence (DeepSeek-V2 shape): for each sequence b and head h,
+/// scores_j = (W_UK^T q_nope . c_j + q_rope . k_rope_j) * sm_scale over the
+/// cache rows j = [c_j ; k_rope_j], softmax, o = W_UV (sum_j p_j c_j).
+pub trait LatentAttention: QuantizedCompute {
+    /// q_nope f32 `[B][H][dn]`, q_rope f32 `[B][H][dr]`, cache bf16
+    /// `[B][L][r + dr]`, w_uk rowwise int8 `[H*r][dn]`, w_uv rowwise int8
+    /// `[H*dv][r]`; returns f32 `[B][H][dv]`.
+    fn mla_decode(&self, q_nope: &Self::Buffer, q_rope: &Self::Buffer, cache: &Self::Buffer, b: usize, h: usize,
+                  l: usize, dn: usize, dr: usize, r: usize, dv: usize, w_uk: &Self::QWeight, w_uv: &Self::QWeight,
+                  sm_scale: f32) -> Self::Buffer;
+}
+
+impl LatentAttention for HipComputeDevice {
+    fn mla_decode(&self, q_nope: &HipBuffer, q_rope: &HipBuffer, cache: &HipBuffer, b: usize, h: usize, l: usize,
+                  dn: usize, dr: usize, r: usize, dv: usize, w_uk: &HipQWeight, w_uv: &HipQWeight,
+                  sm_scale: f32) -> HipBuffer {
+        let out = self.buffer(ffi::TH_F32, b * h * dv);
+        check(unsafe {
+            ffi::th_mla_decode(self.dev, q_nope.raw, q_rope.raw, cache.raw, b, h, l, dn, dr, r, dv, w_uk.raw, w_uv.raw,
+                               sm_scale, out.raw)
+        });
+        out
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MoE layer (no counterpart in the reference)
+// ---------------------------------------------------------------------------
+
+/// The outputs of one MoE forward.
+pub struct MoeOutput {
+    /// f32 `[T][d_model]`.
+    pub out: HipBuffer,
+    /// i32 `[T][top_k]`: routed experts, probability descending (ties: lower index).
+    pub topk_idx: HipBuffer,
+    /// f32 `[T][top_k]`: their softmax probabilities (not renormalised).
+    pub topk_w: HipBuffer,
+}
+
+/// A DeepSeek-style MoE layer: f32 router `[E][d]`, softmax over the router
+/// logits, top-k routed SwiGLU experts weighted by their probabilities, plus
+/// `n_shared` always-on experts; expert linears int4 group-32.
+pub struct HipMoe<'d> {
+    raw: *mut ffi::th_moe,
+    pub d_model: usize,
+    pub top_k: usize,
+    dev: &'d HipComputeDevice,
+}
+
+impl<'d> HipMoe<'d> {
+    pub fn new(dev: &'d HipComputeDevice, d_model: usize, d_ff: usize, n_experts: usize, n_shared: usize,
+               top_k: usize) -> Self {
+        let mut raw = ptr::null_mut();
+        check(unsafe { ffi::th_moe_create(dev.dev, d_model, d_ff, n_experts, n_shared, top_k, &mut raw) });
+        HipMoe { raw, d_model, top_k, dev }
+    }
+
+    /// Seeded synthetic weights (router N(0, 0.02), experts as th_synth_q4).
+    pub fn init_synthetic(&mut self, seed: u64) {
+        check(unsafe { ffi::th_moe_init_synthetic(self.raw, seed) });
+    }
+
+    /// `h`: `[t][d_model]` activations, f32 (rounded to bf16 here) or bf16.
+    pub fn forward(&self, h: &HipBuffer, t: usize) -> MoeOutput {
+        let hb;
+        let h = if h.dtype == ffi::TH_BF16 {
+            h
+        } else {
+            hb = self.dev.convert(h, ffi::TH_BF16);
+            &hb
+        };
+        let out = self.dev.buffer(ffi::TH_F32, t * self.d_model);
+        let topk_idx = self.dev.buffer(ffi::TH_I32, t * self.top_k);
+        let topk_w = self.dev.buffer(ffi::TH_F32, t * self.top_k);
+        check(unsafe { ffi::th_moe_forward(self.raw, h.raw, t, out.raw, topk_idx.raw, topk_w.raw) });
+        MoeOutput { out, topk_idx, topk_w }
+    }
+}
+
+impl Drop for HipMoe<'_> {
+    fn drop(&mut self) {
+        unsafe {
+            ffi::th_moe_destroy(self.raw);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode engine
+// ---------------------------------------------------------------------------
+
+/// The shape of a Llama-style decoder (crates/tang-train/examples/smollm.rs).
+#[derive(Clone, Copy, Debug)]
+pub struct LlamaConfig {
+    pub n_layers: usize,
+    pub d_model: usize,
+    pub n_heads: usize,
+    pub n_kv_heads: usize,
+    pub head_dim: usize,
+    pub d_ff: usize,
+    pub vocab: usize,
+    /// KV cache length: positions 0..max_seq.
+    pub max_seq: usize,
+    pub eps: f32,
+    pub rope_theta: f64,
+}
+
+/// A whole Llama-shaped model resident on the device: int4 group-32 linears,
+/// bf16 embeddings and norms, f16 KV cache; each decode step is one recorded
+/// kernel sequence replayed on the device (the step of smollm.rs:215-300).
+pub struct HipLlama<'d> {
+    raw: *mut ffi::th_llama,
+    cfg: LlamaConfig,
+    _dev: PhantomData<&'d HipComputeDevice>,
+}
+
+fn token_i32(t: usize, vocab: usize) -> i32 {
+    assert!(t < vocab, "token {} out of the vocabulary ({})", t, vocab);
+    t as i32
+}
+
+impl<'d> HipLlama<'d> {
+    pub fn new(dev: &'d HipComputeDevice, cfg: LlamaConfig) -> Self {
+        let c = ffi::th_llama_config {
+            n_layers: cfg.n_layers as c_int,
+            d_model: cfg.d_model as c_int,
+            n_heads: cfg.n_heads as c_int,
+            n_kv_heads: cfg.n_kv_heads as c_int,
+            head_dim: cfg.head_dim as c_int,
+            d_ff: cfg.d_ff as c_int,
+            vocab: cfg.vocab as c_int,
+            max_seq: cfg.max_seq as c_int,
+            eps: cfg.eps,
+            rope_theta: cfg.rope_theta,
+        };
+        let mut raw = ptr::null_mut();
+        check(unsafe { ffi::th_llama_create(dev.dev, &c, &mut raw) });
+        HipLlama { raw, cfg, _dev: PhantomData }
+    }
+
+    pub fn config(&self) -> &LlamaConfig {
+        &self.cfg
+    }
+
+    /// Seeded synthetic weights (the benchmark model of BASELINE config 3).
+    pub fn init_synthetic(&mut self, seed: u64) {
+        check(unsafe { ffi::th_llama_init_synthetic(self.raw, seed) });
+    }
+
+    /// Weights from a safetensors file with the Llama tensor names that
+    /// `load_model` reads (smollm.rs:364-420), quantized to int4 on upload.
+    pub fn load_safetensors(&mut self, path: &Path) {
+        let p = CString::new(path.to_str().expect("path is not UTF-8")).expect("path holds a NUL byte");
+        let mut f = ptr::null_mut();
+        check(unsafe { ffi::th_st_open(p.as_ptr(), &mut f) });
+        let rc = unsafe { ffi::th_llama_load_safetensors(self.raw, f) };
+        unsafe {
+            ffi::th_st_close(f);
+        }
+        check(rc);
+    }
+
+    /// The prompt through every layer at positions pos..pos+n (K/V appended);
+    /// returns the greedy next token and its logits.
+    pub fn prefill(&mut self, tokens: &[usize], pos: usize) -> (usize, Vec<f32>) {
+        let t: Vec<i32> = tokens.iter().map(|&x| token_i32(x, self.cfg.vocab)).collect();
+        let mut next = 0i32;
+        let mut logits = vec![0.0f32; self.cfg.vocab];
+        check(unsafe { ffi::th_llama_prefill(self.raw, t.as_ptr(), t.len(), pos, &mut next, logits.as_mut_ptr()) });
+        (next as usize, logits)
+    }
+
+    /// n_steps greedy decode steps from `token` at `pos`; returns the tokens
+    /// chosen after each step and the last step's logits.
+    pub fn generate_greedy(&mut self, token: usize, pos: usize, n_steps: usize) -> (Vec<usize>, Vec<f32>) {
+        let mut toks = vec![0i32; n_steps];
+        let mut logits = vec![0.0f32; self.cfg.vocab];
+        check(unsafe {
+            ffi::th_llama_generate(self.raw, token_i32(token, self.cfg.vocab), pos, n_steps, toks.as_mut_ptr(),
+                                   logits.as_mut_ptr())
+        });
+        (toks.into_iter().map(|t| t as usize).collect(), logits)
+    }
+
+    /// `tang_infer::generate` (sampling.rs:229-256) on this model from
+    /// position 0: the prompt is prefilled, then each step samples with
+    /// `Sampler::with_seed(config, seed)` (the reference's sampler, restated
+    /// on the host) and decodes on the device, until `max_tokens` tokens or
+    /// the stop token.  Returns prompt + generated tokens, as the reference.
+    pub fn generate(&mut self, prompt: &[usize], config: &SamplingConfig, seed: u64) -> Vec<usize> {
+        assert!(!prompt.is_empty(), "empty prompt");
+        let cfg = ffi::th_sampling_config {
+            temperature: config.temperature,
+            top_k: config.top_k,
+            top_p: config.top_p,
+            repetition_penalty: config.repetition_penalty,
+            stop_token: config.stop_token.map(|t| t as i64).unwrap_or(-1),
+            max_tokens: config.max_tokens,
+        };
+        let p: Vec<i32> = prompt.iter().map(|&x| token_i32(x, self.cfg.vocab)).collect();
+        // all but the last prompt token go through the prefill; the sampled
+        // loop feeds the last one at its position
+        if p.len() > 1 {
+            check(unsafe {
+                ffi::th_llama_prefill(self.raw, p.as_ptr(), p.len() - 1, 0, ptr::null_mut(), ptr::null_mut())
+            });
+        }
+        let mut sampler = ptr::null_mut();
+        check(unsafe { ffi::th_sampler_create(&cfg, seed, &mut sampler) });
+        let mut out = vec![0i32; config.max_tokens];
+        let mut n_out = 0usize;
+        let rc = unsafe {
+            ffi::th_llama_generate_sampled(self.raw, sampler, p.as_ptr(), p.len(), p.len() - 1, out.as_mut_ptr(),
+                                           &mut n_out)
+        };
+        unsafe {
+            ffi::th_sampler_destroy(sampler);
+        }
+        check(rc);
+        let mut tokens = prompt.to_vec();
+        tokens.extend(out[..n_out].iter().map(|&t| t as usize));
+        tokens
+    }
+}
+
+impl Drop for HipLlama<'_> {
+    fn drop(&mut self) {
+        unsafe {
+            ffi::th_llama_destroy(self.raw);
+        }
     }
 }

@@ -136,7 +136,7 @@ def test_elementwise_runtime_kernels(dev):
     for n_in, body, res, ref in cases:
         k = dev.compile_kernel(_expr_kernel(n_in, body, res))
         try:
-            got = dev.elementwise(k, [dx, dy][:n_in], n).to_numpy()
+            got = dev.run_kernel(k, [dx, dy][:n_in], n).to_numpy()
         finally:
             capi.lib().th_kernel_free(k)
         want = ref()
@@ -149,3 +149,69 @@ def test_elementwise_compile_error_reported(dev):
     with pytest.raises(capi.TangHipError) as e:
         dev.compile_kernel('extern "C" __global__ void k0(float* outputs, const unsigned int count) { oops; }')
     assert "compile" in str(e.value)
+
+
+def _graphs():
+    """(n_inputs, builder, exact): graphs over x in [0.1, 3) and y ~ N(0, 1).
+    exact: only +, *, neg, 1/x, sqrt, select and literals, whose f64 results
+    are IEEE-determined, so the device must give the CPU backend's bits."""
+    def hypot_sel(g, v):
+        x, y = v
+        return g.select(y, g.sqrt(g.add(g.mul(x, x), g.mul(y, y))), g.neg(g.recip(x)))
+
+    def poly(g, v):
+        x, y = v
+        t = g.add(g.mul(g.lit(0.1), x), g.lit(-2.5))
+        return g.add(g.mul(t, t), g.mul(g.lit(1.0 / 3.0), g.mul(x, y)))
+
+    def sigmoid_ish(g, v):  # the reference's softplus/sigmoid shapes go through exp2 and recip
+        x, y = v
+        e = g.exp2(g.mul(g.lit(-1.4426950408889634), y))
+        return g.mul(x, g.recip(g.add(g.lit(1.0), e)))
+
+    def trig(g, v):
+        x, y = v
+        return g.add(g.mul(g.sin(x), g.atan2(y, x)), g.log2(x))
+
+    def one_input(g, v):
+        (x,) = v
+        return g.mul(g.add(x, g.lit(1.0)), g.add(x, g.lit(1.0)))
+
+    return [(2, hypot_sel, True), (2, poly, True), (2, sigmoid_ish, False), (2, trig, False), (1, one_input, True)]
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 1027, 100003])
+def test_elementwise_graph_matches_cpu_backend(dev, n):
+    """ComputeDevice::elementwise from a tang-expr graph: bit-identical to the
+    CPU backend's f64 evaluation (oracle.expr_eval) for the IEEE-exact ops;
+    within one f32 rounding step for sin/atan2/exp2/log2 (device math
+    library against the host's libm, both f64).  n covers the 4-wide tail."""
+    import oracle
+    rng = np.random.default_rng(n)
+    x = rng.uniform(0.1, 3.0, n).astype(np.float32)
+    y = rng.standard_normal(n).astype(np.float32)
+    dx, dy = dev.upload(x), dev.upload(y)
+    for n_in, build, exact in _graphs():
+        print("expr", build.__name__, n, flush=True)
+        got = dev.elementwise([dx, dy][:n_in], n, build).to_numpy()
+        g = capi.ExprGraph()
+        out = build(g, [g.var(i) for i in range(n_in)])
+        want = oracle.expr_eval(g.array(), out, [x, y][:n_in])
+        if exact:
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), build.__name__
+        else:
+            ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+            assert ulp.max() <= 1, (build.__name__, ulp.max())
+
+
+def test_elementwise_graph_cache_and_special_values(dev):
+    """The same graph twice (second call from the device's compiled cache),
+    and IEEE special values: 1/0 = inf, sqrt(-1) = NaN, select on NaN takes
+    the else branch, as the CPU backend's closure does."""
+    x = np.array([0.0, -1.0, np.nan, 4.0, -0.0], np.float32)
+    dx = dev.upload(x)
+    build = lambda g, v: g.add(g.recip(v[0]), g.select(v[0], g.sqrt(v[0]), g.lit(7.0)))
+    a = dev.elementwise([dx], len(x), build).to_numpy()
+    b = dev.elementwise([dx], len(x), build).to_numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.isposinf(a[0]) and a[1] == 6.0 and np.isnan(a[2]) and a[3] == 2.25 and np.isneginf(a[4])

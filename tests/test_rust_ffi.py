@@ -11,14 +11,16 @@ th_sampling_config) list the header's fields in order."""
 import os
 import re
 
+import pytest
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "tang_hip.h")
 CRATE = os.path.join(ROOT, "tang_amd", "tang-compute-hip", "src")
 
 C_BASE = {"int": "i32", "size_t": "usize", "float": "f32", "double": "f64", "uint64_t": "u64", "int64_t": "i64",
-          "int32_t": "i32", "uint8_t": "u8", "int8_t": "i8", "uint16_t": "u16", "char": "c_char", "void": "void",
+          "int32_t": "i32", "uint32_t": "u32", "uint8_t": "u8", "int8_t": "i8", "uint16_t": "u16", "char": "c_char", "void": "void",
           "th_dtype": "i32"}
-RUST_BASE = {"c_int": "i32", "usize": "usize", "f32": "f32", "f64": "f64", "u64": "u64", "i64": "i64", "i32": "i32",
+RUST_BASE = {"c_int": "i32", "usize": "usize", "f32": "f32", "f64": "f64", "u64": "u64", "i64": "i64", "i32": "i32", "u32": "u32",
              "u8": "u8", "i8": "i8", "u16": "u16", "c_char": "c_char", "c_void": "void"}
 
 # The required methods of `trait ComputeDevice` (device.rs:19-869): those
@@ -128,3 +130,86 @@ def test_every_entry_point_the_binding_calls_is_declared():
     src = open(os.path.join(CRATE, "lib.rs")).read()
     called = set(re.findall(r"ffi::(th_\w+)\s*\(", src))
     assert called <= set(header_functions()), sorted(called - set(header_functions()))
+
+
+REF_DEVICE = "/root/reference/crates/tang-compute/src/device.rs"
+
+
+def _split_top(s, sep=","):
+    """Split at `sep` outside (), [], <>."""
+    out, depth, cur = [], 0, ""
+    for i, ch in enumerate(s):
+        if ch in "([<":
+            depth += 1
+        elif ch in ")]>" and not (ch == ">" and s[i - 1] == "-"):
+            depth -= 1
+        if ch == sep and depth == 0:
+            out.append(cur)
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip():
+        out.append(cur)
+    return [p.strip() for p in out if p.strip()]
+
+
+def _signatures(src, buffer_names):
+    """{method: (param types, return type)} of every `fn` in src, with the
+    buffer type spelled B and whitespace removed."""
+    sigs = {}
+    for m in re.finditer(r"\bfn\s+(\w+)\s*\(", src):
+        name, i, depth = m.group(1), m.end(), 1
+        while depth:
+            depth += {"(": 1, ")": -1}.get(src[i], 0)
+            i += 1
+        params = src[m.end():i - 1]
+        rest = src[i:]
+        ret = re.match(r"\s*(?:->\s*([^{;]+?))?\s*(?:where[^{;]*)?[{;]", rest, flags=re.S)
+        norm = lambda t: re.sub(r"\s+", "", re.sub(r"\b(%s)\b" % "|".join(buffer_names), "B", t))
+        types = [norm(p.split(":", 1)[1]) for p in _split_top(params) if ":" in p]
+        sigs[name] = (types, norm(ret.group(1) or "()"))
+    return sigs
+
+
+def _trait_body(src, start):
+    i = src.index("{", src.index(start)) + 1
+    depth = 1
+    j = i
+    while depth:
+        depth += {"{": 1, "}": -1}.get(src[j], 0)
+        j += 1
+    return src[i:j - 1]
+
+
+@pytest.mark.skipif(not os.path.exists(REF_DEVICE), reason="the reference checkout is not on this machine")
+def test_implemented_trait_methods_have_the_reference_signatures():
+    """Every method `impl ComputeDevice for HipComputeDevice` defines exists in
+    the reference trait (crates/tang-compute/src/device.rs:19-869) with the
+    same parameter types and return type (Self::Buffer = HipBuffer)."""
+    ref = _signatures(_trait_body(open(REF_DEVICE).read(), "pub trait ComputeDevice"), [r"Self::Buffer"])
+    src = open(os.path.join(CRATE, "lib.rs")).read()
+    ours = _signatures(_trait_body(src, "impl ComputeDevice for HipComputeDevice"), ["HipBuffer"])
+    assert len(ref) > 60 and len(ours) > 40
+    bad = {n: (sig, ref.get(n)) for n, sig in ours.items() if ref.get(n) != sig}
+    assert not bad, bad
+    required = [n for n in ref if re.search(r"\bfn\s+%s\s*\([^{]*?\)\s*(->[^{;]*)?;" % n,
+                                            _trait_body(open(REF_DEVICE).read(), "pub trait ComputeDevice"),
+                                            flags=re.S)]
+    assert sorted(required) == sorted(REQUIRED)
+
+
+def test_extension_wrappers_cover_the_engines():
+    """Safe wrappers exist for every configuration's entry points: the
+    quantized linear, MLA decode, the MoE layer and the decode engine
+    (greedy, prefill, safetensors load, and generate() with the sampler)."""
+    src = open(os.path.join(CRATE, "lib.rs")).read()
+    called = set(re.findall(r"ffi::(th_\w+)\s*\(", src))
+    for fn in ("th_gemm_q4", "th_gemv_q8", "th_q8_upload_rowwise", "th_mla_decode", "th_moe_create",
+               "th_moe_init_synthetic", "th_moe_forward", "th_moe_destroy", "th_llama_create", "th_llama_destroy",
+               "th_llama_init_synthetic", "th_llama_load_safetensors", "th_llama_prefill", "th_llama_generate",
+               "th_llama_generate_sampled", "th_sampler_create", "th_sampler_destroy", "th_elementwise_expr"):
+        assert fn in called, fn
+    for decl in ("pub trait LatentAttention", "pub struct HipMoe", "pub struct HipLlama",
+                 "pub fn generate(&mut self, prompt: &[usize], config: &SamplingConfig, seed: u64) -> Vec<usize>"):
+        assert decl in src, decl
+    assert "Dialect::Cuda" not in src
