@@ -342,6 +342,93 @@ __global__ void prefill_swiglu_kernel(const float* __restrict__ gu, int ff, uint
 // above): one 256-thread workgroup per row stages the row's bf16 values in
 // LDS (dynamic, ldo halves), takes their largest magnitude, then writes the
 // scaled f16 chunks (zero past ff) and the row exponent.
+// RMSNorm into the prepared GEMM layout with the row held in registers:
+// 256 threads per row, U chunks of 8 elements per thread (d <= 2048 * U), so
+// the row is read once (one wave re-reading it per pass was latency-bound:
+// 10 us per 512 rows).  Same arithmetic per element as prefill_rmsnorm_kernel
+// (x * inv * w rounded to bf16, then the row exponent and f16), the sum of
+// squares in a fixed order: per thread over its chunks, then across the block.
+template <int U>
+__global__ __launch_bounds__(256) void prefill_rmsnorm_xp_kernel(const float* __restrict__ x,
+                                                                 const uint16_t* __restrict__ w, int d, float eps,
+                                                                 uint16_t* __restrict__ out, int ldo,
+                                                                 int* __restrict__ xexp) {
+    __shared__ float red_sum[4], red_max[4];
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float* xr = x + (size_t)row * d;
+    float y[U][8];
+    uint4 wv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {  // every load first
+        const int k0 = (t + 256 * u) * 8;
+        if (k0 < d) {
+            const float4 a = *(const float4*)(xr + k0), b = *(const float4*)(xr + k0 + 4);
+            y[u][0] = a.x; y[u][1] = a.y; y[u][2] = a.z; y[u][3] = a.w;
+            y[u][4] = b.x; y[u][5] = b.y; y[u][6] = b.z; y[u][7] = b.w;
+            wv[u] = *(const uint4*)(w + k0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) y[u][i] = 0.0f;
+            wv[u] = make_uint4(0, 0, 0, 0);
+        }
+    }
+    float sq = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) sq += y[u][i] * y[u][i];
+    sq = wave_sum(sq);
+    if ((t & 63) == 0) red_sum[t >> 6] = sq;
+    __syncthreads();
+    const float tot = (red_sum[0] + red_sum[1]) + (red_sum[2] + red_sum[3]);
+    const float inv = 1.0f / sqrtf(tot / (float)d + eps);
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {  // cpu.rs:146: x * inv_rms * w, then the bf16 linear input
+            const uint32_t wbits = (i & 1) ? (ww[i >> 1] >> 16) : (ww[i >> 1] & 0xFFFFu);
+            y[u][i] = bf16_bits_to_f32(f32_to_bf16_rne(y[u][i] * inv * __uint_as_float(wbits << 16)));
+            mx = fmaxf(mx, fabsf(y[u][i]));
+        }
+    }
+    const int e = range_exp(block_absmax256(mx, red_max), XPREP_TOP);
+    if (t == 0) xexp[row] = e;
+    uint16_t* orow = out + (size_t)row * ldo;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int c = t + 256 * u;
+        if (c * 8 >= ldo) continue;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = __builtin_amdgcn_ldexpf(y[u][i], -e);  // zero past d
+        *(uint4*)(orow + c * 8) = make_uint4(pack_half2(v[0], v[4]), pack_half2(v[1], v[5]), pack_half2(v[2], v[6]),
+                                             pack_half2(v[3], v[7]));
+    }
+}
+
+// Gate/up GEMM epilogue of the prefill: the fused weight's 16-row tiles hold
+// 8 gate rows then their 8 up rows, so a gate row's partner is in lane + 32
+// (D rows 4q..4q+3 per lane).  Writes bf16(swiglu(g, u)) (f64 SwiGLU, as the
+// decode epilogue and device.rs:727 via cpu.rs:68) into h[row][ff].
+struct EpiGemmSwiGLU {
+    uint16_t* h;
+    int ff;
+    __device__ __forceinline__ void operator()(int row, int n0, int, bool live, const float4_t& v) const {
+        float up[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) up[i] = __shfl_xor(v[i], 32, 64);
+        const int rr = n0 & 15;
+        if (!live || rr >= 8) return;
+        uint16_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = f32_to_bf16_rne(swiglu_f64(v[i], up[i]));
+        *(uint2*)(h + (size_t)row * ff + (n0 >> 4) * 8 + rr) =
+            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+    }
+};
+
 __global__ __launch_bounds__(256) void prefill_swiglu_xp_kernel(const float* __restrict__ gu, int ff,
                                                                uint16_t* __restrict__ out, int ldo,
                                                                int* __restrict__ xexp) {
@@ -657,6 +744,40 @@ static void prefill_reserve(th_llama* m, size_t rows) {
 
 // One chunk of n prompt tokens at positions pos0.. through every layer; the
 // residual of its rows ends in pf_x.
+// Prepared-layout RMSNorm of n rows of the residual (d <= 8192).
+static void prefill_rmsnorm_xp(const float* x, const uint16_t* w, int d, float eps, uint16_t* out, int ldo,
+                               int* xexp, size_t n, hipStream_t s) {
+    const int chunks = std::max(d, ldo) / 8;
+    if (chunks <= 512)
+        TH_LAUNCH(prefill_rmsnorm_xp_kernel<2>, dim3((unsigned)n), dim3(256), 0, s, x, w, d, eps, out, ldo, xexp);
+    else
+        TH_LAUNCH(prefill_rmsnorm_xp_kernel<4>, dim3((unsigned)n), dim3(256), 0, s, x, w, d, eps, out, ldo, xexp);
+    TH_LAUNCH_CHECK();
+}
+
+// The fused gate/up linear with SwiGLU in its epilogue: h[n][ff] bf16 (no
+// split-K: used from PREFILL_FUSED_SWIGLU_ROWS rows, where the grid covers
+// the chip without it).
+constexpr size_t PREFILL_FUSED_SWIGLU_ROWS = 128;
+static void prefill_gate_up_swiglu(const th_qweight* w, PreparedX xp, size_t n, uint16_t* h, int ff, hipStream_t s) {
+    const size_t NT = w->Np / 16;
+    const int GQ = (int)(w->Kp / 128);
+    GemmDense src;
+    src.M = (int)n;
+    const EpiGemmSwiGLU epi{h, ff};
+    if (n <= 1024)
+        TH_LAUNCH((q4_gemm_mfma_kernel<2, 4, _Float16, GemmDense, EpiGemmSwiGLU>),
+                  dim3((unsigned)ceil_div(NT, (size_t)8), (unsigned)ceil_div(n, (size_t)64), 1), dim3(256), 0, s,
+                  (const uint4*)w->data, (const _Float16*)w->scales, (const int*)w->row_exp, xp.x, xp.xexp, epi, src,
+                  (int)w->rows, (int)w->cols, (int)w->Kp, (int)w->Kp, GQ);
+    else
+        TH_LAUNCH((q4_gemm_mfma_kernel<2, 8, _Float16, GemmDense, EpiGemmSwiGLU>),
+                  dim3((unsigned)ceil_div(NT, (size_t)8), (unsigned)ceil_div(n, (size_t)128), 1), dim3(256), 0, s,
+                  (const uint4*)w->data, (const _Float16*)w->scales, (const int*)w->row_exp, xp.x, xp.xexp, epi, src,
+                  (int)w->rows, (int)w->cols, (int)w->Kp, (int)w->Kp, GQ);
+    TH_LAUNCH_CHECK();
+}
+
 static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t pos0) {
     const th_llama_config& c = m->cfg;
     th_device* dev = m->dev;
@@ -673,7 +794,9 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
     int* xe_att = m->pf_xe + m->pf_rows;
     int* xe_sg = m->pf_xe + 2 * m->pf_rows;
     auto prefill_norm = [&](const uint16_t* w, const th_qweight* consumer) {
-        if (xp)
+        if (xp && d <= 8192 && (int)consumer->Kp <= 8192)
+            prefill_rmsnorm_xp(m->pf_x, w, d, c.eps, m->pf_xb, (int)consumer->Kp, xe_xb, n, s);
+        else if (xp)
             TH_LAUNCH(prefill_rmsnorm_kernel<true>, dim3((unsigned)n), dim3(64), 0, s, m->pf_x, w, d, c.eps,
                                m->pf_xb, (int)consumer->Kp, xe_xb);
         else
@@ -715,6 +838,16 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
             TH_LAUNCH_CHECK();
         }
         prefill_norm(m->ffn_norm + (size_t)l * d, m->wgu[l]);
+        if (xp && n >= PREFILL_FUSED_SWIGLU_ROWS && m->wgu[l]->scale_dtype == TH_F16) {
+            // SwiGLU in the gate/up GEMM's epilogue (bf16 rows in pf_gu's
+            // memory), prepared for the down GEMM by the activation pass, and
+            // x += sg.Wd^T in the down GEMM's epilogue
+            uint16_t* h = (uint16_t*)m->pf_gu;
+            prefill_gate_up_swiglu(m->wgu[l], PreparedX{m->pf_xb, xe_xb}, n, h, ff, s);
+            const PreparedX sg = prepare_x(dev, h, false, n, ff, ff, m->wd[l]->Kp, s);
+            launch_q4_linear_prepared(m->wd[l], sg, n, m->pf_x, d, s, dev, true);
+            continue;
+        }
         linear(m->wgu[l], m->pf_xb, xe_xb, d, m->pf_gu, 2 * ff);
         if (xp) {
             const int ldo = (int)m->wd[l]->Kp;
