@@ -300,22 +300,44 @@ __global__ __launch_bounds__(64) void prefill_rmsnorm_kernel(const float* __rest
 }
 
 // RoPE of q and k (device.rs:582-610, as EpiQKV) at position pos0 + row; q to
-// f32 [n][qd], k and v appended to the f16 cache rows.
-__global__ void prefill_rope_kv_kernel(const float* __restrict__ qkv, int pos0, const float* __restrict__ cs,
-                                       const float* __restrict__ sn, int qd, int kvd, int hd, float* __restrict__ q,
-                                       _Float16* __restrict__ kc, _Float16* __restrict__ vc) {
+// f32 [n][qd], k and v appended to the f16 cache rows.  A thread takes eight
+// consecutive columns (four rotation pairs of one head, never straddling q,
+// k and v) with 16-byte loads and stores; per pair (x0 c - x1 s, x0 s + x1 c).
+__global__ __launch_bounds__(256) void prefill_rope_kv_kernel(const float* __restrict__ qkv, int pos0,
+                                                              const float* __restrict__ cs,
+                                                              const float* __restrict__ sn, int qd, int kvd, int hd,
+                                                              float* __restrict__ q, _Float16* __restrict__ kc,
+                                                              _Float16* __restrict__ vc) {
     const int row = blockIdx.y, W = qd + 2 * kvd, pos = pos0 + row;
-    const float* src = qkv + (size_t)row * W;
-    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < W; n += gridDim.x * blockDim.x) {
-        float out = src[n];
-        if (n < qd + kvd) {
-            const int half = hd / 2, i = (n % hd) >> 1;
-            const float c = cs[(size_t)pos * half + i], s = sn[(size_t)pos * half + i];
-            out = (n & 1) == 0 ? src[n] * c - src[n + 1] * s : src[n - 1] * s + src[n] * c;
+    const int n = (blockIdx.x * 256 + threadIdx.x) * 8;
+    if (n >= W) return;
+    const float* src = qkv + (size_t)row * W + n;
+    const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
+    float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if (n < qd + kvd) {
+        const int half = hd / 2, i0 = (n % hd) >> 1;
+        const float4 c4 = *(const float4*)(cs + (size_t)pos * half + i0);
+        const float4 s4 = *(const float4*)(sn + (size_t)pos * half + i0);
+        const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const float x0 = v[2 * p], x1 = v[2 * p + 1];
+            v[2 * p] = x0 * c[p] - x1 * sv[p];
+            v[2 * p + 1] = x0 * sv[p] + x1 * c[p];
         }
-        if (n < qd) q[(size_t)row * qd + n] = out;
-        else if (n < qd + kvd) kc[(size_t)pos * kvd + (n - qd)] = (_Float16)out;
-        else vc[(size_t)pos * kvd + (n - qd - kvd)] = (_Float16)out;
+    }
+    if (n < qd) {
+        float* dst = q + (size_t)row * qd + n;
+        *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4*)(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+        _Float16* dst = n < qd + kvd ? kc + (size_t)pos * kvd + (n - qd) : vc + (size_t)pos * kvd + (n - qd - kvd);
+        uint32_t h[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+            h[p] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * p]) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * p + 1]) << 16);
+        *(uint4*)dst = make_uint4(h[0], h[1], h[2], h[3]);
     }
 }
 
@@ -817,7 +839,8 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
         _Float16* vc = m->vcache + l * cache_layer;
         prefill_norm(m->attn_norm + (size_t)l * d, m->wqkv[l]);
         linear(m->wqkv[l], m->pf_xb, xe_xb, d, m->pf_qkv, W);
-        TH_LAUNCH(prefill_rope_kv_kernel, dim3(8, (unsigned)n), dim3(256), 0, s, m->pf_qkv, (int)pos0,
+        TH_LAUNCH(prefill_rope_kv_kernel, dim3((unsigned)ceil_div((size_t)W / 8, (size_t)256), (unsigned)n), dim3(256),
+                  0, s, m->pf_qkv, (int)pos0,
                            m->rope_cos, m->rope_sin, m->qd, m->kvd, hd, m->pf_q, kc, vc);
         TH_LAUNCH_CHECK();
         const bool xp_att = xp && (hd == 64 || hd == 128);

@@ -122,10 +122,31 @@ static void q4_span_launch(const th_qweight* w, const void* x, size_t m, size_t 
     }
 }
 
-// Sum KS split-K partials [KS][m][ldy] in split order (then add it to y when
-// add is set: the fused residual add).
-__global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, int M, int N,
-                                     int ldy, int KS, int add) {
+// Sum KS split-K partials [KS][m][N] in split order (then add it to y when
+// add is set: the fused residual add).  VEC4: four consecutive columns per
+// thread with 16-byte accesses (N and ldy multiples of 4); same sums.
+template <bool VEC4>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                            int M, int N, int ldy, int KS, int add) {
+    if (VEC4) {
+        const int N4 = N >> 2;
+        const int total = M * N4;
+        for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+            const int m = i / N4, n = (i - m * N4) * 4;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int s = 0; s < KS; s++) {
+                const float4 p = *(const float4*)(part + ((size_t)s * M + m) * N + n);
+                v.x += p.x; v.y += p.y; v.z += p.z; v.w += p.w;
+            }
+            float4* yp = (float4*)(y + (size_t)m * ldy + n);
+            if (add) {
+                const float4 o = *yp;
+                v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+            }
+            *yp = v;
+        }
+        return;
+    }
     const size_t total = (size_t)M * N;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
         const size_t m = i / N, n = i - m * N;
@@ -194,9 +215,13 @@ static void q4_mfma_launch(const th_qweight* w, PreparedX xp, size_t m, float* y
     TH_LAUNCH_CHECK();
     if (ks > 1) {
         const size_t total = m * w->rows;
-        unsigned blocks = (unsigned)std::min<size_t>(ceil_div(total, 256), 4096);
-        TH_LAUNCH(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, out, y, (int)m, (int)w->rows,
-                           (int)ldy, (int)ks, (int)accumulate);
+        const bool vec4 = w->rows % 4 == 0 && ldy % 4 == 0 && ((uintptr_t)y & 15) == 0 && total < (1u << 31);
+        if (vec4)
+            TH_LAUNCH(splitk_reduce_kernel<true>, dim3((unsigned)std::min<size_t>(ceil_div(total / 4, 256), 4096)),
+                      dim3(256), 0, s, out, y, (int)m, (int)w->rows, (int)ldy, (int)ks, (int)accumulate);
+        else
+            TH_LAUNCH(splitk_reduce_kernel<false>, dim3((unsigned)std::min<size_t>(ceil_div(total, 256), 4096)),
+                      dim3(256), 0, s, out, y, (int)m, (int)w->rows, (int)ldy, (int)ks, (int)accumulate);
         TH_LAUNCH_CHECK();
     }
 }
