@@ -766,6 +766,42 @@ static void prefill_reserve(th_llama* m, size_t rows) {
 
 // One chunk of n prompt tokens at positions pos0.. through every layer; the
 // residual of its rows ends in pf_x.
+// QKV GEMM epilogue of the prefill: RoPE on the q and k columns (each lane
+// holds four consecutive columns, i.e. two rotation pairs, of one row), q to
+// f32 [n][qd], k and v appended to the f16 cache at pos0 + row -- the
+// arithmetic of prefill_rope_kv_kernel, without the f32 qkv round trip.
+struct EpiGemmQKVRope {
+    float* q;
+    _Float16 *kc, *vc;
+    const float *cs, *sn;
+    int pos0, qd, kvd, hd;
+    __device__ __forceinline__ void operator()(int row, int n0, int N, bool live, const float4_t& v) const {
+        if (!live || n0 >= N) return;
+        const int pos = pos0 + row;
+        float o[4] = {v[0], v[1], v[2], v[3]};
+        if (n0 < qd + kvd) {
+            const int half = hd / 2, i0 = (n0 % hd) >> 1;
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const float c = cs[(size_t)pos * half + i0 + p], sv = sn[(size_t)pos * half + i0 + p];
+                const float x0 = o[2 * p], x1 = o[2 * p + 1];
+                o[2 * p] = x0 * c - x1 * sv;
+                o[2 * p + 1] = x0 * sv + x1 * c;
+            }
+        }
+        if (n0 < qd) {
+            *(float4*)(q + (size_t)row * qd + n0) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+            _Float16* dst = n0 < qd + kvd ? kc + (size_t)pos * kvd + (n0 - qd) : vc + (size_t)pos * kvd + (n0 - qd - kvd);
+            const uint32_t h0 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)o[0]) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)o[1]) << 16);
+            const uint32_t h1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)o[2]) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)o[3]) << 16);
+            *(uint2*)dst = make_uint2(h0, h1);
+        }
+    }
+};
+
 // Prepared-layout RMSNorm of n rows of the residual (d <= 8192).
 static void prefill_rmsnorm_xp(const float* x, const uint16_t* w, int d, float eps, uint16_t* out, int ldo,
                                int* xexp, size_t n, hipStream_t s) {
@@ -777,23 +813,22 @@ static void prefill_rmsnorm_xp(const float* x, const uint16_t* w, int d, float e
     TH_LAUNCH_CHECK();
 }
 
-// The fused gate/up linear with SwiGLU in its epilogue: h[n][ff] bf16 (no
-// split-K: used from PREFILL_FUSED_SWIGLU_ROWS rows, where the grid covers
-// the chip without it).
-constexpr size_t PREFILL_FUSED_SWIGLU_ROWS = 128;
-static void prefill_gate_up_swiglu(const th_qweight* w, PreparedX xp, size_t n, uint16_t* h, int ff, hipStream_t s) {
+// A prefill linear with its epilogue fused (no split-K: used from
+// PREFILL_FUSED_ROWS rows, where the grid covers the chip without it).
+constexpr size_t PREFILL_FUSED_ROWS = 256;
+template <typename Epi>
+static void prefill_gemm_epi(const th_qweight* w, PreparedX xp, size_t n, const Epi& epi, hipStream_t s) {
     const size_t NT = w->Np / 16;
     const int GQ = (int)(w->Kp / 128);
     GemmDense src;
     src.M = (int)n;
-    const EpiGemmSwiGLU epi{h, ff};
     if (n <= 1024)
-        TH_LAUNCH((q4_gemm_mfma_kernel<2, 4, _Float16, GemmDense, EpiGemmSwiGLU>),
+        TH_LAUNCH((q4_gemm_mfma_kernel<2, 4, _Float16, GemmDense, Epi>),
                   dim3((unsigned)ceil_div(NT, (size_t)8), (unsigned)ceil_div(n, (size_t)64), 1), dim3(256), 0, s,
                   (const uint4*)w->data, (const _Float16*)w->scales, (const int*)w->row_exp, xp.x, xp.xexp, epi, src,
                   (int)w->rows, (int)w->cols, (int)w->Kp, (int)w->Kp, GQ);
     else
-        TH_LAUNCH((q4_gemm_mfma_kernel<2, 8, _Float16, GemmDense, EpiGemmSwiGLU>),
+        TH_LAUNCH((q4_gemm_mfma_kernel<2, 8, _Float16, GemmDense, Epi>),
                   dim3((unsigned)ceil_div(NT, (size_t)8), (unsigned)ceil_div(n, (size_t)128), 1), dim3(256), 0, s,
                   (const uint4*)w->data, (const _Float16*)w->scales, (const int*)w->row_exp, xp.x, xp.xexp, epi, src,
                   (int)w->rows, (int)w->cols, (int)w->Kp, (int)w->Kp, GQ);
@@ -834,15 +869,25 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
     const size_t attended = pos0 + n;
     const int subs = (int)std::max<size_t>(1, ceil_div(attended, (size_t)ATTN_SUB * 8));
     const int n_splits = (int)ceil_div(attended, (size_t)subs * ATTN_SUB);
+    // From PREFILL_FUSED_ROWS rows: RoPE/KV append in the QKV GEMM epilogue,
+    // SwiGLU in the gate/up GEMM epilogue (engine weights: f16 scales)
+    const bool fused = xp && n >= PREFILL_FUSED_ROWS && m->wqkv[0]->scale_dtype == TH_F16 &&
+                       m->wgu[0]->scale_dtype == TH_F16;
     for (int l = 0; l < c.n_layers; l++) {
         _Float16* kc = m->kcache + l * cache_layer;
         _Float16* vc = m->vcache + l * cache_layer;
         prefill_norm(m->attn_norm + (size_t)l * d, m->wqkv[l]);
+        if (fused) {  // RoPE and the K/V append in the QKV GEMM's epilogue
+            prefill_gemm_epi(m->wqkv[l], PreparedX{m->pf_xb, xe_xb}, n,
+                             EpiGemmQKVRope{m->pf_q, kc, vc, m->rope_cos, m->rope_sin, (int)pos0, m->qd, m->kvd, hd},
+                             s);
+        } else {
         linear(m->wqkv[l], m->pf_xb, xe_xb, d, m->pf_qkv, W);
         TH_LAUNCH(prefill_rope_kv_kernel, dim3((unsigned)ceil_div((size_t)W / 8, (size_t)256), (unsigned)n), dim3(256),
                   0, s, m->pf_qkv, (int)pos0,
                            m->rope_cos, m->rope_sin, m->qd, m->kvd, hd, m->pf_q, kc, vc);
         TH_LAUNCH_CHECK();
+        }
         const bool xp_att = xp && (hd == 64 || hd == 128);
         if (hd == 64 || hd == 128) {  // causal flash attention on MFMA
             launch_attn_prefill(m->pf_q, m->qd, kc, vc, c.n_heads, c.n_kv_heads, hd, (int)pos0, (int)n,
@@ -861,12 +906,12 @@ static void prefill_chunk(th_llama* m, const int32_t* tok_host, size_t n, size_t
             TH_LAUNCH_CHECK();
         }
         prefill_norm(m->ffn_norm + (size_t)l * d, m->wgu[l]);
-        if (xp && n >= PREFILL_FUSED_SWIGLU_ROWS && m->wgu[l]->scale_dtype == TH_F16) {
+        if (fused) {
             // SwiGLU in the gate/up GEMM's epilogue (bf16 rows in pf_gu's
             // memory), prepared for the down GEMM by the activation pass, and
             // x += sg.Wd^T in the down GEMM's epilogue
             uint16_t* h = (uint16_t*)m->pf_gu;
-            prefill_gate_up_swiglu(m->wgu[l], PreparedX{m->pf_xb, xe_xb}, n, h, ff, s);
+            prefill_gemm_epi(m->wgu[l], PreparedX{m->pf_xb, xe_xb}, n, EpiGemmSwiGLU{h, ff}, s);
             const PreparedX sg = prepare_x(dev, h, false, n, ff, ff, m->wd[l]->Kp, s);
             launch_q4_linear_prepared(m->wd[l], sg, n, m->pf_x, d, s, dev, true);
             continue;
