@@ -587,6 +587,10 @@ inline void launch_attn_split(const float* q, const void* kc, const void* vc, bo
     }
 }
 
+// Threads of a decode-attention workgroup: NT when the split's SPL positions
+// divide into whole passes of NT / (D / 8) keys, else 256.
+constexpr int attn_decode_nt(int D, int SPL, int NT) { return SPL % (NT / (D / 8)) == 0 ? NT : 256; }
+
 // Decode attention for the engine: one query, f16 cache, SPL positions per
 // split; counters (n_heads ints) zero on entry and on return.
 template <int SPL, bool OUT_BF16, int NT = 256, bool EVEN = false>
@@ -597,9 +601,9 @@ inline void launch_attn_decode(const float* q, const _Float16* kc, const _Float1
     const dim3 grid((unsigned)n_heads, 1, (unsigned)n_splits);
     const size_t lds = 0;
     switch (head_dim) {
-        case 64: TH_LAUNCH((attn_decode_kernel<64, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 128: TH_LAUNCH((attn_decode_kernel<128, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
-        case 256: TH_LAUNCH((attn_decode_kernel<256, SPL, OUT_BF16, NT, EVEN>), grid, dim3(NT), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 64: TH_LAUNCH((attn_decode_kernel<64, SPL, OUT_BF16, attn_decode_nt(64, SPL, NT), EVEN>), grid, dim3(attn_decode_nt(64, SPL, NT)), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 128: TH_LAUNCH((attn_decode_kernel<128, SPL, OUT_BF16, attn_decode_nt(128, SPL, NT), EVEN>), grid, dim3(attn_decode_nt(128, SPL, NT)), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
+        case 256: TH_LAUNCH((attn_decode_kernel<256, SPL, OUT_BF16, attn_decode_nt(256, SPL, NT), EVEN>), grid, dim3(attn_decode_nt(256, SPL, NT)), lds, s, q, kc, vc, n_heads, n_kv_heads, n_splits, part, counters, out, cache_start_dev); break;
         default: throw Error(TH_ERR_INVALID, "launch_attn_decode: unsupported head_dim");
     }
     TH_LAUNCH_CHECK();
