@@ -1149,25 +1149,35 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     for (int a = 0; a < RT; a++) wneg[a] = -wexp[min(tile0 + a, NT - 1) * 16 + r];
 
     const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(xin, 0x7FFFFFF0u);  // in-range offsets only
-    // staging assignment: CB*16 cols * 16 chunks (4 groups x 4 quads) = CB*256 chunks
+    // staging assignment: CB*16 cols * 16 chunks (4 groups x 4 quads) = CB*256 chunks.
+    // A thread's chunks keep their row and their place in the group-quad
+    // over the whole K loop: their offsets (for the grouped source, after the
+    // slot -> token lookup) are formed once, so no step waits on that lookup.
+    uint32_t xoff[CB];   // halves: row * ldx + j * 32 + qq * 8
+    bool xlive[CB];
+#pragma unroll
+    for (int i = 0; i < CB; i++) {
+        const int idx = tid + i * 256;  // chunk id
+        const int col = idx & 15, qq = (idx >> 4) & 3, j = (idx >> 6) & 3, cb = idx >> 8;
+        const int ml = cb * 16 + col;
+        if constexpr (Src::GROUPED) {  // short work items: skip the loads of empty rows
+            xlive[i] = ml < mrows;
+            xoff[i] = (uint32_t)((xlive[i] ? src.x_row(ml) : 0) * ldx + j * 32 + qq * 8);
+        } else {
+            // branch-free: rows past mrows re-read the last live row (a finite
+            // copy whose D columns are never stored)
+            xlive[i] = true;
+            xoff[i] = (uint32_t)(src.x_row(min(ml, mrows - 1)) * ldx + j * 32 + qq * 8);
+        }
+    }
     auto load_x = [&](int gq, uint4 (&regs)[CB]) {
 #pragma unroll
         for (int i = 0; i < CB; i++) {
-            const int idx = tid + i * 256;        // chunk id
-            const int col = idx & 15;
-            const int qq = (idx >> 4) & 3;
-            const int j = (idx >> 6) & 3;
-            const int cb = idx >> 8;
-            const int ml = cb * 16 + col;
-            const int k0 = gq * 128 + j * 32 + qq * 8;
-            if constexpr (Src::GROUPED) {  // short work items: skip the loads of empty rows
-                regs[i] = ml < mrows ? *(const uint4*)(xin + (size_t)src.x_row(ml) * ldx + k0)
-                                     : make_uint4(0, 0, 0, 0);
+            const uint32_t off = xoff[i] + (uint32_t)gq * 128u;
+            if constexpr (Src::GROUPED) {
+                regs[i] = xlive[i] ? *(const uint4*)(xin + off) : make_uint4(0, 0, 0, 0);
             } else {
-                // branch-free: rows past mrows re-read the last live row
-                // (a finite copy whose D columns are never stored)
-                const uint32_t off = (uint32_t)(src.x_row(min(ml, mrows - 1)) * ldx + k0) * 2u;
-                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off * 2u, 0, 0);
                 regs[i] = make_uint4(v.x, v.y, v.z, v.w);
             }
         }
