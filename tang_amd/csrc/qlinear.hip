@@ -166,6 +166,25 @@ PreparedX prepare_x(th_device* dev, const void* x, bool xf32, size_t m, size_t l
     const size_t xbytes = round_up(m * Kp * 2, 256);
     char* ws = workspace ? (char*)workspace : (char*)device_scratch_x(dev, prepared_x_bytes(m, Kp));
     PreparedX p{(const uint16_t*)ws, (const int*)(ws + xbytes)};
+    const size_t cpr = Kp / 8;
+    if (cpr <= 8 * 256) {  // row per workgroup, in registers
+        auto row_kernel = [&](auto xf, auto u) {
+            constexpr bool XF = decltype(xf)::value;
+            constexpr int UU = decltype(u)::value;
+            TH_LAUNCH((q4_gemm_xprep_row_kernel<XF, UU>), dim3((unsigned)m), dim3(256), 0, s, x, (int)ldx, (int)K,
+                      (int)Kp, rows, (uint4*)ws, (int*)(ws + xbytes));
+        };
+        auto by_u = [&](auto xf) {
+            if (cpr <= 256) row_kernel(xf, std::integral_constant<int, 1>{});
+            else if (cpr <= 512) row_kernel(xf, std::integral_constant<int, 2>{});
+            else if (cpr <= 1024) row_kernel(xf, std::integral_constant<int, 4>{});
+            else row_kernel(xf, std::integral_constant<int, 8>{});
+        };
+        if (xf32) by_u(std::true_type{});
+        else by_u(std::false_type{});
+        TH_LAUNCH_CHECK();
+        return p;
+    }
     const unsigned grid = (unsigned)ceil_div(m, (size_t)4);
     if (xf32)
         TH_LAUNCH((q4_gemm_xprep_kernel<true>), dim3(grid), dim3(256), 0, s, x, (int)ldx, (int)K, (int)Kp,

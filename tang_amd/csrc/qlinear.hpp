@@ -1105,6 +1105,47 @@ __global__ __launch_bounds__(256) void q4_gemm_xprep_kernel(const void* __restri
     }
 }
 
+// The same layout with one 256-thread workgroup per row and the row held in
+// registers (U chunks of 8 per thread, Kp <= 2048 * U): one read of the row
+// instead of two passes by one wave.  Identical output (the row maximum does
+// not depend on the order).
+template <bool XF32, int U>
+__global__ __launch_bounds__(256) void q4_gemm_xprep_row_kernel(const void* __restrict__ xin, int ldx, int K, int Kp,
+                                                                const int* __restrict__ rows, uint4* __restrict__ out,
+                                                                int* __restrict__ xexp) {
+    __shared__ float red4[4];
+    const int r = blockIdx.x, t = threadIdx.x;
+    const int row = rows ? rows[r] : r;
+    const int cpr = Kp >> 3;
+    const bool vec = (ldx & 7) == 0 && (((uintptr_t)xin) & 15) == 0;
+    float xv[U][8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int c = t + 256 * u;
+        if (c < cpr) {
+            xprep_load8<XF32>(xin, (size_t)ldx, row, K, c * 8, vec, xv[u]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) xv[u][e] = 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(xv[u][e]));
+    }
+    const int e = range_exp(block_absmax256(mx, red4), XPREP_TOP);
+    if (t == 0) xexp[r] = e;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int c = t + 256 * u;
+        if (c >= cpr) continue;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = __builtin_amdgcn_ldexpf(xv[u][i], -e);
+        out[(size_t)r * cpr + c] = make_uint4(pack_half2(v[0], v[4]), pack_half2(v[1], v[5]), pack_half2(v[2], v[6]),
+                                              pack_half2(v[3], v[7]));
+    }
+}
+
 // xin: prepared rows (f16, ldx = Kp halves, row exponents xexp); wexp: the
 // weight rows' scale exponents (th_qweight::row_exp).
 template <int RT, int CB, typename ST, typename Src = GemmDense, typename Epi = EpiGemmStore>
