@@ -297,6 +297,11 @@ int th_kv_attention(th_device* dev, const th_buffer* q, const th_buffer* k_cache
                     size_t n_kv_heads, size_t head_dim, th_buffer* out);
 /* swiglu_fused_buf (device.rs:727): out = g*sigmoid(g)*u. */
 int th_swiglu(th_device* dev, const th_buffer* gate, const th_buffer* up, size_t n, th_buffer* out);
+/* swiglu_fused_buf (device.rs:727) as a linear's input: out (bf16) =
+ * bf16(f32(g*sigmoid(g)*u)) with the cuda.rs:22 rounding -- the SwiGLU the
+ * decode, prefill and MoE epilogues apply; the same bits as th_swiglu's f32
+ * output rounded to bf16. */
+int th_swiglu_bf16(th_device* dev, const th_buffer* gate, const th_buffer* up, size_t n, th_buffer* out);
 /* add_tensors_buf (device.rs:721). */
 int th_add(th_device* dev, const th_buffer* a, const th_buffer* b, size_t n, th_buffer* out);
 /* CpuDevice::embedding (cpu.rs:151): weight f32 or bf16 [vocab][dim], ids u32. */

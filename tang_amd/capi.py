@@ -82,6 +82,7 @@ SIGNATURES = {
     "th_rope_forward": ([_P, _P, _P, _P, _S, _S, _S, _S, _P], _I),
     "th_kv_attention": ([_P, _P, _P, _P, _S, _S, _S, _S, _S, _P], _I),
     "th_swiglu": ([_P, _P, _P, _S, _P], _I),
+    "th_swiglu_bf16": ([_P, _P, _P, _S, _P], _I),
     "th_add": ([_P, _P, _P, _S, _P], _I),
     "th_embedding": ([_P, _P, _P, _S, _S, _P], _I),
     "th_softmax": ([_P, _P, _S, _S, _P], _I),

@@ -123,7 +123,7 @@ struct EpiSwiGLU : EpiNoFinish {
     uint16_t* out;
     __device__ __forceinline__ void operator()(int, int n, float v, const float* tile, float*) const {
         const int rr = n & 15;
-        if (rr < 8) st_coherent(&out[(n >> 4) * 8 + rr], f32_to_bf16_rne(swiglu_f64(v, tile[rr + 8])));
+        if (rr < 8) st_coherent(&out[(n >> 4) * 8 + rr], swiglu_bf16(v, tile[rr + 8]));
     }
 };
 
@@ -356,7 +356,7 @@ __global__ void prefill_swiglu_kernel(const float* __restrict__ gu, int ff, uint
     uint16_t* orow = out + (size_t)row * ldo;
     for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < ff; j += gridDim.x * blockDim.x) {
         const int b = j >> 3, rr = j & 7;
-        orow[j] = f32_to_bf16_rne(swiglu_f64(g[16 * b + rr], g[16 * b + 8 + rr]));
+        orow[j] = swiglu_bf16(g[16 * b + rr], g[16 * b + 8 + rr]);
     }
 }
 
@@ -445,7 +445,7 @@ struct EpiGemmSwiGLU {
         if (!live || rr >= 8) return;
         uint16_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) o[i] = f32_to_bf16_rne(swiglu_f64(v[i], up[i]));
+        for (int i = 0; i < 4; i++) o[i] = swiglu_bf16(v[i], up[i]);
         *(uint2*)(h + (size_t)row * ff + (n0 >> 4) * 8 + rr) =
             make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
     }
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256) void prefill_swiglu_xp_kernel(const float* __r
         uint16_t hb = 0;
         if (j < ff) {
             const int b = j >> 3, rr = j & 7;
-            hb = f32_to_bf16_rne(swiglu_f64(g[16 * b + rr], g[16 * b + 8 + rr]));
+            hb = swiglu_bf16(g[16 * b + rr], g[16 * b + 8 + rr]);
             mx = fmaxf(mx, fabsf(bf16_bits_to_f32(hb)));
         }
         hrow[j] = hb;

@@ -60,6 +60,12 @@ __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restri
         out[i] = swiglu_f64(g[i], u[i]);
 }
 
+__global__ void swiglu_bf16_kernel(const float* __restrict__ g, const float* __restrict__ u, size_t n,
+                                   uint16_t* __restrict__ out) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = swiglu_bf16(g[i], u[i]);
+}
+
 __global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, size_t n, float* __restrict__ out) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         out[i] = a[i] + b[i];
@@ -228,6 +234,19 @@ int th_swiglu(th_device* dev, const th_buffer* g, const th_buffer* u, size_t n, 
     if (n == 0) return TH_OK;
     TH_LAUNCH(swiglu_kernel, dim3(grid_for(n)), dim3(256), 0, dev->stream, (const float*)g->ptr,
                        (const float*)u->ptr, n, (float*)out->ptr);
+    TH_LAUNCH_CHECK();
+    TH_API_END
+}
+
+int th_swiglu_bf16(th_device* dev, const th_buffer* g, const th_buffer* u, size_t n, th_buffer* out) {
+    TH_API_BEGIN
+    TH_REQUIRE(dev && g && u && out, "null argument");
+    require_len(g, TH_F32, n, "gate");
+    require_len(u, TH_F32, n, "up");
+    require_len(out, TH_BF16, n, "out");
+    if (n == 0) return TH_OK;
+    TH_LAUNCH(swiglu_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, dev->stream, (const float*)g->ptr,
+              (const float*)u->ptr, n, (uint16_t*)out->ptr);
     TH_LAUNCH_CHECK();
     TH_API_END
 }

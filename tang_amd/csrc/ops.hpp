@@ -158,6 +158,23 @@ __device__ __forceinline__ float swiglu_f64(float g, float u) {
     return (float)(gd * sig * (double)u);
 }
 
+// bf16 (cuda.rs:22 rule) of swiglu_f64(g, u), the rounding every consumer of
+// a SwiGLU output applies (it is a linear input).  Evaluated in f32 -- expf,
+// one division and two products stay within a few f32 ulps of the f64 value
+// -- and the f32 result decides the bf16 rounding unless it lies within 64
+// ulps of a bf16 rounding midpoint (or is tiny or not finite), where the f64
+// evaluation decides.  So the bits are always those of
+// f32_to_bf16_rne(swiglu_f64(g, u)); the f64 path runs for ~0.2% of inputs.
+__device__ __forceinline__ uint16_t swiglu_bf16(float g, float u) {
+    const float s = 1.0f / (1.0f + expf(-g));
+    const float y = g * s * u;
+    const uint32_t lo = __float_as_uint(y) & 0xFFFFu;
+    const float ay = fabsf(y);
+    if (ay >= 0x1p-100f && ay <= 0x1p+100f && (lo + 64u < 0x8000u || lo > 0x8000u + 64u))
+        return f32_to_bf16_rne(y);
+    return f32_to_bf16_rne(swiglu_f64(g, u));
+}
+
 // First-maximum argmax over one row with a 256-thread block
 // (crates/tang-infer/src/sampling.rs:184-194: strict '>' keeps the lowest index).
 __device__ __forceinline__ void argmax_block_256(const float* x, int n, float* rv, int* ri, float& bv_out, int& bi_out) {

@@ -202,6 +202,7 @@ extern "C" {
     pub fn th_rope_forward(dev: *mut th_device, in_: *const th_buffer, cos_buf: *const th_buffer, sin_buf: *const th_buffer, seq_len: usize, n_heads: usize, head_dim: usize, start_pos: usize, out: *mut th_buffer) -> c_int;
     pub fn th_kv_attention(dev: *mut th_device, q: *const th_buffer, k_cache: *const th_buffer, v_cache: *const th_buffer, cache_start: usize, q_len: usize, n_heads: usize, n_kv_heads: usize, head_dim: usize, out: *mut th_buffer) -> c_int;
     pub fn th_swiglu(dev: *mut th_device, gate: *const th_buffer, up: *const th_buffer, n: usize, out: *mut th_buffer) -> c_int;
+    pub fn th_swiglu_bf16(dev: *mut th_device, gate: *const th_buffer, up: *const th_buffer, n: usize, out: *mut th_buffer) -> c_int;
     pub fn th_add(dev: *mut th_device, a: *const th_buffer, b: *const th_buffer, n: usize, out: *mut th_buffer) -> c_int;
     pub fn th_embedding(dev: *mut th_device, weight: *const th_buffer, ids: *const th_buffer, seq_len: usize, dim: usize, out: *mut th_buffer) -> c_int;
     pub fn th_softmax(dev: *mut th_device, x: *const th_buffer, n_rows: usize, row_len: usize, out: *mut th_buffer) -> c_int;

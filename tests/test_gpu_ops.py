@@ -58,6 +58,30 @@ def test_swiglu_add(dev):
     assert np.array_equal(s, oracle.add(g, u))
 
 
+def test_swiglu_bf16_equals_f64_path_rounded(dev):
+    """th_swiglu_bf16 (the f32 evaluation the epilogues use, with the f64
+    evaluation near bf16 rounding midpoints) gives exactly the bits of the
+    f64 path (th_swiglu) rounded to bf16 by the cuda.rs:22 rule, over 6M
+    inputs: N(0, 3) gates, gates over [-120, 120] with up values from 1e-30
+    to 1e30 (underflow, overflow of exp), and special values."""
+    rng = np.random.default_rng(11)
+    n1, n2 = 4 << 20, 2 << 20
+    g = np.concatenate([rng.standard_normal(n1) * 3, rng.uniform(-120, 120, n2),
+                        [0.0, -0.0, 1e-40, -1e-40, 88.0, -88.0, 104.0, -104.0, np.inf, -np.inf, np.nan, 1.0]])
+    u = np.concatenate([rng.standard_normal(n1), rng.choice([-1, 1], n2) * 10.0 ** rng.uniform(-30, 30, n2),
+                        [1.0, 1.0, 1.0, -1.0, 1e-30, 1e30, 3.0, -3.0, 1.0, 1.0, 1.0, np.inf]])
+    g, u = g.astype(np.float32), u.astype(np.float32)
+    n = len(g)
+    dg, du = dev.upload(g), dev.upload(u)
+    f = dev.swiglu_fused_buf(dg, du, n).to_numpy()
+    out = dev.alloc(n, capi.BF16)
+    capi.check(capi.lib().th_swiglu_bf16(dev.handle, dg.handle, du.handle, n, out.handle))
+    got = out.to_numpy()
+    want = oracle.f32_to_bf16(f)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, (bad[:5], g[bad[:5]], u[bad[:5]], got[bad[:5]], want[bad[:5]])
+
+
 def test_embedding(dev):
     w = np.array([0.1, 0.2, 0.3, 0.4, 0.5, 0.6], np.float32)
     out = dev.embedding(dev.upload(w), dev.upload_u32([2, 0, 1]), 3, 2).to_numpy()
