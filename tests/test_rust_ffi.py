@@ -110,8 +110,8 @@ def _fields_c(struct_src):
 def test_repeated_structs_match_header():
     src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
     rs = open(os.path.join(CRATE, "ffi.rs")).read()
-    for name in ("th_q4_block", "th_q8_block", "th_llama_config", "th_sampling_config"):
-        m = re.search(r"typedef struct \{([^}]*)\}\s*" + name + ";", src)
+    for name in ("th_q4_block", "th_q8_block", "th_llama_config", "th_sampling_config", "th_expr_node"):
+        m = re.search(r"typedef struct (?:\w+ )?\{([^}]*)\}\s*" + name + ";", src)
         c_fields = _fields_c(m.group(1))
         m2 = re.search(r"pub struct " + name + r" \{([^}]*)\}", rs)
         r_fields = re.findall(r"pub (\w+):", m2.group(1))
