@@ -42,6 +42,8 @@ __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
 // Cache-policy bit of a gfx950 vector memory access that makes it coherent
 // across XCDs (the bit the relaxed agent-scope atomics above carry).
 constexpr int CPOL_SC1 = 16;
+// Non-temporal (streaming) bit of the same cache-policy field.
+constexpr int CPOL_NT = 2;
 // dword 3 of a raw (untyped) buffer resource.
 constexpr int BUFFER_RSRC_W3 = 0x00020000;
 

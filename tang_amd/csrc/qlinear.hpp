@@ -414,6 +414,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 
     const uint4* wp = wt + (size_t)t * GQ * 64 + lane;
     auto item_gq = [&](int i) { return i < nmine ? wave + NW * i : 0; };
+    // The weight stream of the plain-output GEMV up to 8 rows as buffer loads
+    // off one scalar base (the byte offset per lane in a VGPR) with the
+    // non-temporal bit, else non-temporal global loads.  Same-box A/B of the
+    // two forms (whatever the other cache bits): config 2 M=1 5.84 against
+    // 5.95 us, M=8 7.80 against 8.19, M=4 equal, but M=16 9.1-9.3 against
+    // 8.9 and the decode step's fused-epilogue GEMVs 0.3% slower.
+    constexpr bool BUF_W = MR <= 8 && !NORM && std::is_same<Epi, EpiStore>::value;
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wt, 0xFFFFFFFFu);
+    auto load_item = [&](int i) -> uint4 {
+        if constexpr (BUF_W) {
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+                wrs, (uint32_t)(((size_t)t * GQ * 64 + lane + (size_t)item_gq(i) * 64) * 16), 0, CPOL_NT);
+            return make_uint4(v.x, v.y, v.z, v.w);
+        } else {
+            return ldg_stream(wt + (size_t)t * GQ * 64 + lane + (size_t)item_gq(i) * 64);
+        }
+    };
     auto scale_ptr_t = [&](int i, int tile) -> const typename SR::Rec* {
         const int gq = item_gq(i);  // past the end: a valid record of this tile
         const int g0 = (F16S && NW == 4) ? (gq & ~4) : gq;
@@ -483,7 +500,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
     for (int u = 0; u < D; u++) {
         if (u % SI == 0) sbuf[u / SI] = load_scale(u);
-        wbuf[u] = ldg_stream(wp + (size_t)item_gq(u) * 64);
+        wbuf[u] = load_item(u);
         if constexpr (PAR > 1) {
 #pragma unroll
             for (int pp = 0; pp < PAR - 1; pp++) {
@@ -765,7 +782,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
             const typename SR::Rec sv = scur;
             if constexpr (decltype(refill_tag)::value == 1) {
                 if (u % SI == 0) sbuf[u / SI] = load_scale(i + D);
-                wbuf[u] = ldg_stream(wp + (size_t)item_gq(i + D) * 64);
+                wbuf[u] = load_item(i + D);
             } else if constexpr (decltype(refill_tag)::value == 2) {
                 // past the last tile the refill reads the activations (hot
                 // in L2, never used): a re-read of this tile's own items
