@@ -1184,6 +1184,22 @@ __global__ __launch_bounds__(256) void q4_gemm_xprep_row_kernel(const void* __re
     }
 }
 
+// Workgroup -> (weight block, activation block) of a one-plane GEMM grid.
+// Linear workgroup i runs on XCD i mod 8; this hands each XCD a contiguous
+// range of tiles, walked in bands of 8 activation blocks, so the workgroups
+// resident on one XCD share 8 activation and 8 weight blocks in its L2.
+__device__ __forceinline__ void gemm_xcd_tile(int& bx, int& by) {
+    const int gx = gridDim.x, gy = gridDim.y, W = gx * gy;
+    const int L = blockIdx.x + gx * blockIdx.y;
+    const int k = L & 7;
+    const int t = k * (W >> 3) + min(k, W & 7) + (L >> 3);
+    constexpr int G = 8;
+    const int band = t / (G * gx), rows = min(G, gy - band * G);
+    const int v = t - band * G * gx;
+    bx = v / rows;
+    by = band * G + v % rows;
+}
+
 // xin: prepared rows (f16, ldx = Kp halves, row exponents xexp); wexp: the
 // weight rows' scale exponents (th_qweight::row_exp).
 template <int RT, int CB, typename ST, typename Src = GemmDense, typename Epi = EpiGemmStore>
@@ -1196,12 +1212,15 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     // two B tiles: the next group-quad's is written while this one is read,
     // so one barrier per step orders both
     __shared__ uint4 bt2[2][CB * 4 * 4 * 16];
-    int mrows = 0;
+    int mrows = 0, tile_blk = 0;
     {
         const uint4* wsel = wt;
         const ST* ssel = sc;
         const int* esel = wexp;
-        if (!src.select((int)blockIdx.y, CB * 16, wsel, ssel, esel, mrows)) return;
+        int bx = blockIdx.x, by = blockIdx.y;
+        if (!Src::GROUPED && gridDim.z == 1) gemm_xcd_tile(bx, by);
+        tile_blk = bx;
+        if (!src.select(by, CB * 16, wsel, ssel, esel, mrows)) return;
         wt = wsel;
         sc = ssel;
         wexp = esel;
@@ -1212,7 +1231,7 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = Src::GROUPED ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int q = lane >> 4, r = lane & 15;
-    const int tile0 = (blockIdx.x * 4 + wave) * RT;  // first 16-row tile of this wave
+    const int tile0 = (tile_blk * 4 + wave) * RT;  // first 16-row tile of this wave
     const int NT = (N + 15) >> 4;
     const int gq0 = blockIdx.z * gq_per_split;
     const int gq1 = min(GQ, gq0 + gq_per_split);
