@@ -421,11 +421,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE))) 
     // 5.95 us, M=8 7.80 against 8.19, M=4 equal, but M=16 9.1-9.3 against
     // 8.9 and the decode step's fused-epilogue GEMVs 0.3% slower.
     constexpr bool BUF_W = MR <= 8 && !NORM && std::is_same<Epi, EpiStore>::value;
-    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wt, 0xFFFFFFFFu);
+    // based at the tile (t is uniform), so the offsets stay below GQ KiB for
+    // any matrix size
+    const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(wt + (size_t)t * GQ * 64, 0xFFFFFFFFu);
     auto load_item = [&](int i) -> uint4 {
         if constexpr (BUF_W) {
             const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
-                wrs, (uint32_t)(((size_t)t * GQ * 64 + lane + (size_t)item_gq(i) * 64) * 16), 0, CPOL_NT);
+                wrs, (uint32_t)(lane + item_gq(i) * 64) * 16u, 0, CPOL_NT);
             return make_uint4(v.x, v.y, v.z, v.w);
         } else {
             return ldg_stream(wt + (size_t)t * GQ * 64 + lane + (size_t)item_gq(i) * 64);
