@@ -35,7 +35,7 @@ GEMV_BYTES = {1: 25414656, 4: 25571328, 8: 25780224, 16: 26198016}  # algorithmi
 N_COPIES = 12  # 12 x 25.4 MB = 305 MB > 256 MB last-level cache
 # HBM bytes per M=1 launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE runs in
 # profiles/q4_gemv_config2.md, each scaled by its reading of a known-size copy.
-TRAFFIC_BYTES = 25563136
+TRAFFIC_BYTES = 25547776
 
 CFG7B = dict(n_layers=32, d_model=4096, n_heads=32, n_kv_heads=32, head_dim=128, d_ff=11008, vocab=32000,
              max_seq=2176, eps=1e-5, rope_theta=1e4)
