@@ -1069,11 +1069,12 @@ struct GemmDense {
 struct EpiGemmStore {
     float* y;
     int ldy;
-    size_t split_stride;  // split-K partials: y + blockIdx.z * split_stride
+    size_t split_stride;  // split-K partials: y + split * split_stride
     int add = 0;          // y += v (a residual add, device.rs:721) instead of y = v
+    int split = 0;        // this workgroup's K split (set by the kernel)
     __device__ __forceinline__ void operator()(int out_row, int n0, int N, bool live, const float4_t& v) const {
         if (!live) return;
-        float* yb = y + (size_t)blockIdx.z * split_stride + (size_t)out_row * ldy;
+        float* yb = y + (size_t)split * split_stride + (size_t)out_row * ldy;
 #pragma unroll
         for (int i = 0; i < 4; i++)
             if (n0 + i < N) yb[n0 + i] = add ? yb[n0 + i] + v[i] : v[i];
@@ -1186,20 +1187,23 @@ __global__ __launch_bounds__(256) void q4_gemm_xprep_row_kernel(const void* __re
     }
 }
 
-// Workgroup -> (weight block, activation block) of a one-plane GEMM grid.
-// Linear workgroup i runs on XCD i mod 8; this hands each XCD a contiguous
-// range of tiles, walked in bands of 8 activation blocks, so the workgroups
-// resident on one XCD share 8 activation and 8 weight blocks in its L2.
-__device__ __forceinline__ void gemm_xcd_tile(int& bx, int& by) {
-    const int gx = gridDim.x, gy = gridDim.y, W = gx * gy;
-    const int L = blockIdx.x + gx * blockIdx.y;
+// Workgroup -> (weight block, activation block, K split) of a dense GEMM
+// grid.  Linear workgroup i runs on XCD i mod 8; this hands each XCD a
+// contiguous range of tiles of the (x, y + gy * z) plane, walked in bands of
+// 8 activation blocks, so the workgroups resident on one XCD share 8
+// activation and 8 weight blocks in its L2.
+__device__ __forceinline__ void gemm_xcd_tile(int& bx, int& by, int& bz) {
+    const int gx = gridDim.x, gy = gridDim.y, gyz = gy * gridDim.z, W = gx * gyz;
+    const int L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
     const int k = L & 7;
     const int t = k * (W >> 3) + min(k, W & 7) + (L >> 3);
     constexpr int G = 8;
-    const int band = t / (G * gx), rows = min(G, gy - band * G);
+    const int band = t / (G * gx), rows = min(G, gyz - band * G);
     const int v = t - band * G * gx;
     bx = v / rows;
-    by = band * G + v % rows;
+    const int yz = band * G + v % rows;
+    bz = yz / gy;
+    by = yz - bz * gy;
 }
 
 // xin: prepared rows (f16, ldx = Kp halves, row exponents xexp); wexp: the
@@ -1214,13 +1218,13 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     // two B tiles: the next group-quad's is written while this one is read,
     // so one barrier per step orders both
     __shared__ uint4 bt2[2][CB * 4 * 4 * 16];
-    int mrows = 0, tile_blk = 0;
+    int mrows = 0, tile_blk = 0, split = blockIdx.z;
     {
         const uint4* wsel = wt;
         const ST* ssel = sc;
         const int* esel = wexp;
         int bx = blockIdx.x, by = blockIdx.y;
-        if (!Src::GROUPED && gridDim.z == 1) gemm_xcd_tile(bx, by);
+        if constexpr (!Src::GROUPED) gemm_xcd_tile(bx, by, split);
         tile_blk = bx;
         if (!src.select(by, CB * 16, wsel, ssel, esel, mrows)) return;
         wt = wsel;
@@ -1235,7 +1239,8 @@ __global__ __launch_bounds__(256) void q4_gemm_mfma_kernel(const uint4* __restri
     const int q = lane >> 4, r = lane & 15;
     const int tile0 = (tile_blk * 4 + wave) * RT;  // first 16-row tile of this wave
     const int NT = (N + 15) >> 4;
-    const int gq0 = blockIdx.z * gq_per_split;
+    const int gq0 = split * gq_per_split;
+    if constexpr (std::is_same<Epi, EpiGemmStore>::value) epi.split = split;
     const int gq1 = min(GQ, gq0 + gq_per_split);
 
     float4_t acc[RT][CB];
