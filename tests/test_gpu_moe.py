@@ -11,7 +11,7 @@ from tang_amd import capi
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("T", [1, 16, 40, 100, 257, 512])  # > 64 tokens: grouped MFMA GEMM; 512: config 4 prefill
+@pytest.mark.parametrize("T", [1, 16, 40, 64, 65, 100, 257, 512])  # > 64 tokens: grouped MFMA GEMM; 512: config 4 prefill
 def test_moe_matches_oracle(dev, T):
     cfg = CONFIG4
     print(f"moe T={T}", flush=True)
